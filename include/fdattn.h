@@ -1,0 +1,215 @@
+/*
+ * fdattn.h -- C ABI of the MI355X (gfx950) split decode-attention library
+ * (libfdattn.so).
+ *
+ * The library implements the three kernels of vllm_fastdecode's split
+ * decode-attention path as hand-written HIP for CDNA4:
+ *
+ *   1. paged partial decode attention over a subset of a sequence's KV
+ *      blocks, emitting (out, lse);
+ *   2. the log-sum-exp merge of two partials (GPU tier + host tier);
+ *   3. the reshape_and_cache slot-mapping write into a paged KV cache.
+ *
+ * The same kernels serve both tiers of the reference's G+C block space: the
+ * HBM tier (vLLM's [num_blocks, block_size, kv_heads, 2*head_size] cache) and
+ * the host tier ([num_blocks, kv_heads, block_size, head_size] in pinned host
+ * memory that the GPU reads and writes zero-copy). Layouts are described by
+ * element strides, so one entry point covers both.
+ *
+ * Conventions shared by every entry point:
+ *   - All buffers are caller-owned; nothing is allocated, and outputs are
+ *     written in place (cpu_attn.cpp:452-489 and :491-517 contract).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
+ *     and the call returns without synchronising.
+ *   - Arguments are validated on the host before any launch; an invalid call
+ *     returns a non-zero status, writes nothing, and leaves a message for
+ *     fd_last_error() (mirrors the TORCH_CHECKs of cpu_attn.cpp:433-477 and the
+ *     "check every slot before any write" rule of cpu_attn.cpp:506-510).
+ *   - Device pointers may point at HBM or at mapped pinned host memory
+ *     (see fd_host_alloc / fd_host_device_pointer).
+ *   - Strides are in elements, not bytes. The innermost (head_size)
+ *     dimension must be contiguous and 16-byte aligned for the fast kernels;
+ *     other layouts take a slower generic kernel.
+ */
+#ifndef FDATTN_H_
+#define FDATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the reference supports fp16, bf16 and fp32 KV:
+ * cpu_attn.cpp:439-448). */
+enum fd_dtype { FD_F16 = 0, FD_BF16 = 1, FD_F32 = 2 };
+
+/* Status codes. */
+enum fd_status {
+  FD_OK = 0,
+  FD_ERR_INVALID = 1,     /* bad shape, stride, dtype or pointer */
+  FD_ERR_RANGE = 2,       /* slot or block id outside the cache */
+  FD_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  FD_ERR_HIP = 4,         /* a HIP runtime call failed */
+  FD_ERR_UNSUPPORTED = 5  /* valid but not implemented (e.g. head_size) */
+};
+
+/* Message describing the last failed call on this host thread
+ * (the reference reports errors as RuntimeError via TORCH_CHECK). */
+const char* fd_last_error(void);
+
+/* Library ABI version (bumped when a signature changes). */
+int fd_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Paged partial decode attention.
+ *
+ * Replaces both implementations of the partial in the reference:
+ *   - the host-tier kernel decode_attn (fastdecode/csrc/cpu_attn.cpp:452-489,
+ *     body :298-411), called at fastdecode/backend.py:350-351;
+ *   - the GPU-tier FlashAttention paged decode
+ *     (flash_attn_varlen_func with max_seqlen_q=1, return_softmax_lse=True,
+ *     fastdecode/backend.py:305-316).
+ *
+ * For every sequence i < n and query head h < num_heads:
+ *   out[i, h, :] = softmax(scale * q[i, h] . K_i^T) @ V_i
+ *   lse[h, i]    = logsumexp(scale * q[i, h] . K_i^T)      (natural log)
+ * over the lens[i] tokens held in blocks block_table[i, 0 .. ceil(lens[i] /
+ * block_size)), in that order; only the last listed block may be partial and
+ * no table entry past it is read. q head h attends kv head
+ * h / (num_heads / num_kv_heads). A row with lens[i] <= 0 yields out = 0 and
+ * lse = -inf (cpu_attn.cpp:324-331). Accumulation is fp32.
+ *
+ * q           [n, num_heads, head_size], dtype kv_dtype, strides
+ *             (q_stride_seq, q_stride_head, 1)
+ * k_cache,
+ * v_cache     paged caches of kv_dtype; token t of block b, kv head g starts
+ *             at b*kv_stride_block + g*kv_stride_head + t*kv_stride_token.
+ *             Host tier [C, KVH, BS, D]: (KVH*BS*D, BS*D, D).
+ *             vLLM HBM tier [B, BS, KVH, 2D] K/V halves: (BS*KVH*2D, 2D, KVH*2D).
+ * num_blocks  blocks in the cache; a table entry outside [0, num_blocks) or
+ *             lens[i] > bt_width*block_size is a device-side range error: the
+ *             row's out and lse become NaN instead of reading out of bounds.
+ * block_table int32 [n, >= bt_width], row stride bt_stride
+ * lens        int32 [n]
+ * out         [n, num_heads, head_size] of out_dtype (kv_dtype or FD_F32),
+ *             strides (out_stride_seq, out_stride_head, 1)
+ * lse         fp32, lse[h, i] at h*lse_stride_head + i
+ * workspace   device scratch of >= fd_paged_decode_workspace_size(...) bytes
+ *             (may be NULL when that size is 0)
+ * ------------------------------------------------------------------------ */
+int fd_paged_decode_partial(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* Bytes of workspace fd_paged_decode_partial needs for these sizes (the
+ * block-range split partials). No counterpart in the reference: its CPU
+ * kernel keeps per-thread scratch in std::vector (cpu_attn.cpp:314-318). */
+int fd_paged_decode_workspace_size(
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, int32_t bt_width, size_t* bytes);
+
+/* ------------------------------------------------------------------------
+ * Log-sum-exp merge of two partials.
+ *
+ * Replaces vLLM's merge_attn_states(out, o_a, lse_a, o_b, lse_b) called at
+ * fastdecode/backend.py:53-55,354-355, with the rule of the reference's torch
+ * restatement merge_partials_torch (fastdecode/cpu_ops.py:93-113):
+ *   lse := -inf where lse == +inf (FlashAttention's "empty");
+ *   m = max(lse_a, lse_b); both empty => m = 0 and the weights' sum is 1,
+ *   giving out = 0;
+ *   w_x = exp(lse_x - m) / (exp(lse_a - m) + exp(lse_b - m));
+ *   out = o_a * w_a + o_b * w_b   (fp32), converted to out_dtype.
+ * out_lse (optional, may be NULL) receives m + log(sum of weights), i.e. the
+ * lse of the merged partial (-inf when both are empty).
+ * o_a, o_b and out are [n, num_heads, head_size] with strides
+ * (stride_seq, stride_head, 1); lse_a, lse_b and out_lse are fp32 indexed
+ * [h * lse_stride_head + i].
+ * ------------------------------------------------------------------------ */
+int fd_merge_attn_states(
+    void* out, int64_t out_stride_seq, int64_t out_stride_head, int32_t out_dtype,
+    const void* o_a, int64_t a_stride_seq, int64_t a_stride_head, int32_t a_dtype,
+    const float* lse_a, int64_t lse_a_stride_head,
+    const void* o_b, int64_t b_stride_seq, int64_t b_stride_head, int32_t b_dtype,
+    const float* lse_b, int64_t lse_b_stride_head,
+    float* out_lse, int64_t out_lse_stride_head,
+    int32_t n, int32_t num_heads, int32_t head_size,
+    void* stream);
+
+/* ------------------------------------------------------------------------
+ * reshape_and_cache: slot-mapping write of this step's K/V rows.
+ *
+ * Replaces vLLM's reshape_and_cache_flash (fastdecode/backend.py:49-51,
+ * 270-273) for the HBM tier and the host-tier store_kv
+ * (fastdecode/csrc/cpu_attn.cpp:491-517, body :413-431) for the pinned host
+ * tier. For every token j < num_tokens with s = slot_mapping[j]:
+ *   s < 0                 skipped (padding / other tier, plan.py:152);
+ *   0 <= s < num_blocks*block_size
+ *                         k_cache[s / block_size, token s % block_size, g, :]
+ *                           = key[j, g, :]   for every kv head g (same for V);
+ *   s >= num_blocks*block_size
+ *                         not written; counted into *error_count when
+ *                         error_count != NULL (a device int32).
+ * The copy is bit-exact. key/value strides are per token and per head
+ * (the rows may be strided views of a fused qkv tensor).
+ * cache strides: element offset of (block b, token t, head g) is
+ *   b*cache_stride_block + t*cache_stride_token + g*cache_stride_head.
+ * slot_mapping is int64 and must be device-readable.
+ * ------------------------------------------------------------------------ */
+int fd_reshape_and_cache(
+    const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+    const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+    void* k_cache, void* v_cache,
+    int64_t cache_stride_block, int64_t cache_stride_token,
+    int64_t cache_stride_head, int64_t num_blocks,
+    const int64_t* slot_mapping, int32_t num_tokens,
+    int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+    int32_t dtype, int32_t* error_count,
+    void* stream);
+
+/* Host-side range check of host-resident slots before a write, the rule of
+ * cpu_attn.cpp:506-510: every slot must lie in [0, capacity). Returns FD_OK,
+ * or FD_ERR_RANGE with *first_bad (if not NULL) set to the first offending
+ * index. Pure host code; never touches the GPU. */
+int fd_check_slots(const int64_t* slots, int64_t m, int64_t capacity,
+                   int64_t* first_bad);
+
+/* ------------------------------------------------------------------------
+ * Pinned host memory for the host tier.
+ *
+ * The reference keeps the host tier in pageable torch.zeros tensors and
+ * stages every per-layer transfer through pinned buffers
+ * (fastdecode/state.py:66-71, :93-124). Here the tier itself is allocated
+ * pinned and mapped (hipHostMalloc), so the kernels above read and write it
+ * directly over the link with no staging copy.
+ * ------------------------------------------------------------------------ */
+int fd_host_alloc(size_t bytes, void** host_ptr);
+int fd_host_free(void* host_ptr);
+/* Device address of a pinned allocation made by fd_host_alloc. */
+int fd_host_device_pointer(void* host_ptr, void** device_ptr);
+
+/* ------------------------------------------------------------------------
+ * Measurement helper: streams `bytes` (a multiple of 16) from src to dst with
+ * the same 16-byte vector loads the attention kernel uses. Used to calibrate
+ * the HBM-traffic counters and the achievable copy bandwidth. No counterpart
+ * in the reference.
+ * ------------------------------------------------------------------------ */
+int fd_stream_copy(void* dst, const void* src, size_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FDATTN_H_ */

@@ -1,0 +1,130 @@
+"""Seeded input generators shared by the tests, the smoke check and bench.py.
+
+`rand_case` follows the reference's test generator _rand_case
+(tests/test_cpu_kernel.py:14-35): q, K pool, V pool drawn as fp32 N(0,1) from
+one seeded CPU generator and cast, lens uniform with lens[0] = max_len and
+lens[1] = 1, and each row's blocks a slice of a random permutation of the pool
+(a fresh permutation when the current one runs out).
+
+`workload` builds the decode-attention workloads of the headline shapes:
+  "correctness"  n=8, 32/32 heads, D=128, BS=16, fp16, pool 1024 blocks,
+                 L ~ U[128, 1024]
+  "vicuna7b"     n=128, 32/32 heads, D=128, BS=16, fp16, L ~ U[256, 2048],
+                 pool = sum of the rows' blocks
+  "llama3_8b"    n=256, 32/8 heads (GQA 4), D=128, BS=16, bf16,
+                 L ~ U[1024, 4096], pool = sum of the rows' blocks
+Large pools are drawn on the GPU with a seeded generator (CPU draws of
+gigabytes would take minutes); everything else is drawn on the CPU.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+def rand_case(n, H, KVH, D, BS, C, dtype, max_len, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(n, H, D, generator=g).to(dtype)
+    k_cache = torch.randn(C, KVH, BS, D, generator=g).to(dtype)
+    v_cache = torch.randn(C, KVH, BS, D, generator=g).to(dtype)
+    lens = torch.randint(0, max_len + 1, (n,), generator=g, dtype=torch.int32)
+    lens[0] = max_len
+    if n > 1:
+        lens[1] = 1
+    W = (max_len + BS - 1) // BS
+    perm = torch.randperm(C, generator=g)
+    bt = torch.zeros(n, W, dtype=torch.int32)
+    pos = 0
+    for i in range(n):
+        nb = (int(lens[i]) + BS - 1) // BS
+        if pos + nb > C:
+            perm = torch.randperm(C, generator=g)
+            pos = 0
+        bt[i, :nb] = perm[pos : pos + nb].to(torch.int32)
+        pos += nb
+    return q, k_cache, v_cache, bt, lens
+
+
+@dataclass
+class Workload:
+    name: str
+    n: int
+    H: int
+    KVH: int
+    D: int
+    BS: int
+    dtype: torch.dtype
+    lo: int
+    hi: int
+    pool: int | None  # fixed pool size, or None = sum of the rows' blocks
+    seed: int
+
+    @property
+    def scale(self) -> float:
+        return 1.0 / math.sqrt(self.D)
+
+
+WORKLOADS = {
+    "correctness": Workload("correctness", 8, 32, 32, 128, 16, torch.float16, 128, 1024, 1024, 0),
+    "vicuna7b": Workload("vicuna7b", 128, 32, 32, 128, 16, torch.float16, 256, 2048, None, 2),
+    "llama3_8b": Workload("llama3_8b", 256, 32, 8, 128, 16, torch.bfloat16, 1024, 4096, None, 3),
+}
+
+
+def draw_lens_and_tables(w: Workload):
+    """lens [n] int32 and a block table [n, W] int32 (W = ceil(hi / BS)); each
+    row's blocks are distinct ids of the pool. Returns (lens, bt, pool)."""
+    g = torch.Generator().manual_seed(w.seed)
+    lens = torch.randint(w.lo, w.hi + 1, (w.n,), generator=g, dtype=torch.int32)
+    nb = (lens + w.BS - 1) // w.BS
+    W = (w.hi + w.BS - 1) // w.BS
+    pool = w.pool if w.pool is not None else int(nb.sum())
+    bt = torch.zeros(w.n, W, dtype=torch.int32)
+    if w.pool is None:
+        perm = torch.randperm(pool, generator=g).to(torch.int32)
+        pos = 0
+        for i in range(w.n):
+            k = int(nb[i])
+            bt[i, :k] = perm[pos : pos + k]
+            pos += k
+    else:
+        for i in range(w.n):
+            k = int(nb[i])
+            bt[i, :k] = torch.randperm(pool, generator=g)[:k].to(torch.int32)
+    return lens, bt, pool
+
+
+def kv_pool(w: Workload, pool: int, layout: str, device, seed_offset: int = 0):
+    """K and V caches of `pool` blocks with N(0,1) values.
+
+    layout "host": separate [pool, KVH, BS, D] tensors (the reference's host
+    tier). layout "vllm": one [pool, BS, KVH, 2D] tensor whose K / V halves
+    are returned as [pool, BS, KVH, D] views (vLLM's HBM tier).
+    """
+    g = torch.Generator(device=device).manual_seed(1000 + w.seed + seed_offset)
+    if layout == "host":
+        k = torch.randn(pool, w.KVH, w.BS, w.D, generator=g, device=device, dtype=torch.float32).to(w.dtype)
+        v = torch.randn(pool, w.KVH, w.BS, w.D, generator=g, device=device, dtype=torch.float32).to(w.dtype)
+        return k, v, None
+    if layout == "vllm":
+        kv = torch.empty(pool, w.BS, w.KVH, 2 * w.D, dtype=w.dtype, device=device)
+        # fill in slabs to bound the fp32 temporary
+        step = max(1, (1 << 28) // (w.BS * w.KVH * 2 * w.D))
+        for s in range(0, pool, step):
+            e = min(pool, s + step)
+            kv[s:e] = torch.randn(e - s, w.BS, w.KVH, 2 * w.D, generator=g, device=device).to(w.dtype)
+        return kv[..., : w.D], kv[..., w.D :], kv
+    raise ValueError(layout)
+
+
+def queries(w: Workload, device) -> torch.Tensor:
+    g = torch.Generator().manual_seed(500 + w.seed)
+    return torch.randn(w.n, w.H, w.D, generator=g).to(w.dtype).to(device)
+
+
+def kv_bytes(lens: torch.Tensor, KVH: int, D: int, elt: int) -> int:
+    """Algorithmic K+V bytes of one partial: 2 * KVH * D * elt per token."""
+    return int(lens.clamp(min=0).sum()) * 2 * KVH * D * elt

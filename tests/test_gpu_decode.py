@@ -1,0 +1,218 @@
+"""GPU parity of the paged partial decode kernel against the float64 oracle.
+
+Tolerances (stated per the path's contract):
+  * fp32 output: max |out - oracle| <= 2e-3 (fp16/bf16 KV, fp32 accumulation);
+  * output in the KV dtype: the reference's own tolerances for a 16-bit
+    result (tests/test_cpu_kernel.py:53): fp16 2e-3, bf16 1.6e-2 (atol and
+    rtol), fp32 KV 1e-5;
+  * lse: |lse - oracle| <= 1e-4 * max(1, |oracle|)  (1e-4 relative);
+  * empty rows: out exactly 0 and lse exactly -inf (cpu_attn.cpp:324-331).
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import pytest
+import torch
+
+import oracle
+from tests import cases
+from vllm_fastdecoder_amd import ops
+from vllm_fastdecoder_amd.pinned import pinned_empty
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL_16BIT = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}
+
+
+def assert_lse_close(lse, ref, mask=None):
+    lse = lse.double().cpu()
+    ref = ref.double()
+    if mask is not None:
+        lse, ref = lse[:, mask], ref[:, mask]
+    err = (lse - ref).abs() / ref.abs().clamp(min=1.0)
+    assert float(err.max()) <= 1e-4, f"lse rel err {float(err.max()):.3g}"
+
+
+def assert_out_close(out, ref, atol, rtol=0.0, mask=None):
+    out = out.double().cpu()
+    if mask is not None:
+        out, ref = out[mask], ref[mask]
+    err = (out - ref).abs() - rtol * ref.abs()
+    assert float(err.max()) <= atol, f"out err {float(err.max()):.3g} > {atol}"
+
+
+def run_host_layout(q, kc, vc, bt, lens, scale, out_dtype, dev):
+    n, H, D = q.shape
+    out = torch.empty(n, H, D, dtype=out_dtype, device=dev)
+    lse = torch.empty(H, n, dtype=torch.float32, device=dev)
+    ops.decode_attn(q.to(dev), kc.to(dev), vc.to(dev), bt.to(dev), lens.to(dev), scale, out, lse)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,KVH", [(8, 8), (8, 2), (4, 1)])
+@pytest.mark.parametrize("D", [64, 128, 72])
+def test_decode_attn_matches_oracle(gpu, dtype, H, KVH, D):
+    """The reference's kernel grid (tests/test_cpu_kernel.py:38-57)."""
+    n, BS, C = 7, 16, 64
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=93, seed=D + H)
+    lens[3] = 0
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    for out_dtype in (dtype, torch.float32):
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, out_dtype, gpu)
+        if out_dtype == torch.float32 and dtype != torch.float32:
+            assert_out_close(out, ref_out, 2e-3, mask=nz)
+        else:
+            tol = OUT_TOL_16BIT[dtype]
+            assert_out_close(out, ref_out, tol, tol, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
+def test_decode_attn_large_scores(gpu):
+    """q x 300: max subtraction keeps everything finite (test_cpu_kernel.py:60-72)."""
+    for dtype, D in ((torch.float32, 64), (torch.float16, 128)):
+        n, H, KVH, BS, C = 2, 4, 4, 16, 8
+        q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float32, 40, 0)
+        q = (q * 300.0).to(dtype)
+        kc, vc = kc.to(dtype), vc.to(dtype)
+        ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, 1.0)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, 1.0, torch.float32, gpu)
+        assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+        assert_out_close(out, ref_out, 1e-3 if dtype == torch.float16 else 1e-4)
+        assert float((lse.double().cpu() - ref_lse).abs().max()) <= 1e-3 * float(ref_lse.abs().max())
+
+
+@pytest.mark.parametrize("split", ["0", "1", "2", "3", "8", "64"])
+def test_correctness_workload_all_splits(gpu, split, monkeypatch):
+    """Config "correctness" (n=8, 32/32, D=128, fp16, pool 1024, L~U[128,1024])
+    with fp32 out, for several block-range split sizes (0 = heuristic)."""
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    k, v, _ = cases.kv_pool(w, pool, "host", "cpu")
+    q = cases.queries(w, "cpu")
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, k, v, bt, lens, w.scale)
+    out, lse = run_host_layout(q, k, v, bt, lens, w.scale, torch.float32, gpu)
+    assert_out_close(out, ref_out, 2e-3)
+    assert_lse_close(lse, ref_lse)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H,KVH", [(32, 32), (32, 8), (16, 2)])
+def test_paged_decode_vllm_layout(gpu, dtype, H, KVH):
+    """HBM-tier layout [B, BS, KVH, 2D] through the FA-style entry, with a
+    padded, junk-filled table past each row's end (never read)."""
+    w = cases.Workload("t", 6, H, KVH, 128, 16, dtype, 1, 300, 64, 11)
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    lens[2] = 0
+    bt_pad = torch.randint(-(10**6), 10**6, (w.n, bt.shape[1] + 7), dtype=torch.int32)
+    for i in range(w.n):
+        nb = (int(lens[i]) + 15) // 16
+        bt_pad[i, :nb] = bt[i, :nb]
+    kc, vc, kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    ref_out, ref_lse, st = oracle.decode_attn_f64(q, kc, vc, oracle.VLLM_DIMS, bt_pad, lens, w.scale)
+    assert st == 0
+    out32 = torch.empty(w.n, H, 128, dtype=torch.float32, device=gpu)
+    o, l = ops.paged_decode(q, kc, vc, bt_pad.to(gpu), lens.to(gpu), w.scale, out=out32)
+    o16, l16 = ops.paged_decode(q, kc, vc, bt_pad.to(gpu), lens.to(gpu), w.scale)
+    torch.cuda.synchronize()
+    nz = lens > 0
+    assert_out_close(o, ref_out, 2e-3)
+    assert_lse_close(l, ref_lse, mask=nz)
+    tol = OUT_TOL_16BIT[dtype]
+    assert_out_close(o16, ref_out, tol, tol)
+    assert torch.equal(l, l16)
+    assert torch.all(torch.isneginf(l[:, 2]))
+
+
+def test_pinned_host_tier_bit_identical(gpu):
+    """The host tier read zero-copy from pinned memory gives exactly the HBM
+    result (same kernel, same inputs)."""
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    k, v, _ = cases.kv_pool(w, pool, "host", "cpu")
+    q = cases.queries(w, gpu)
+    hk = pinned_empty(k.shape, k.dtype)
+    hv = pinned_empty(v.shape, v.dtype)
+    hk.copy_(k)
+    hv.copy_(v)
+    outs = []
+    for kc, vc in ((hk, hv), (k.to(gpu), v.to(gpu))):
+        out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+        lse = torch.empty(w.H, w.n, dtype=torch.float32, device=gpu)
+        ops.decode_attn(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out, lse)
+        outs.append((out, lse))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_range_errors_poison_only_their_rows(gpu):
+    """A table entry outside the cache, or a length beyond the table, turns
+    that row into NaN without touching memory outside the cache; other rows
+    are unaffected."""
+    n, H, KVH, D, BS, C = 4, 8, 8, 128, 16, 16
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float16, 64, 5)
+    lens[:] = torch.tensor([64, 40, 33, 17], dtype=torch.int32)
+    bt[1, 1] = C + 5  # past the cache
+    lens_bad = lens.clone()
+    lens_bad[2] = bt.shape[1] * BS + 1  # beyond the table
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens_bad, 1 / math.sqrt(D))
+    out, lse = run_host_layout(q, kc, vc, bt, lens_bad, 1 / math.sqrt(D), torch.float32, gpu)
+    assert torch.isnan(out[1]).all() and torch.isnan(lse[:, 1]).all()
+    assert torch.isnan(out[2]).all() and torch.isnan(lse[:, 2]).all()
+    ok = torch.tensor([True, False, False, True])
+    assert_out_close(out, ref_out, 2e-3, mask=ok)
+    assert_lse_close(lse, ref_lse, mask=ok)
+
+
+def test_all_empty_and_zero_rows(gpu):
+    n, H, KVH, D, BS, C = 3, 4, 2, 64, 16, 4
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.bfloat16, 20, 1)
+    lens.zero_()
+    out, lse = run_host_layout(q, kc, vc, bt, lens, 0.125, torch.bfloat16, gpu)
+    assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+    # n == 0 is a no-op
+    ops.decode_attn(q[:0].to(gpu), kc.to(gpu), vc.to(gpu), bt[:0].to(gpu), lens[:0].to(gpu), 0.1,
+                    out[:0], lse[:, :0])
+
+
+def test_invalid_arguments_raise_before_writing(gpu):
+    n, H, KVH, D, BS, C = 2, 6, 4, 64, 16, 4  # 6 % 4 != 0
+    q, kc, vc, bt, lens = cases.rand_case(n, H, 2, D, BS, C, torch.float16, 20, 1)
+    kc4 = torch.zeros(C, KVH, BS, D, dtype=torch.float16, device=gpu)
+    out = torch.full((n, H, D), 7.0, device=gpu)
+    lse = torch.full((H, n), 7.0, device=gpu)
+    with pytest.raises(RuntimeError):
+        ops.decode_attn(q.to(gpu), kc4, kc4, bt.to(gpu), lens.to(gpu), 0.1, out, lse)
+    with pytest.raises(RuntimeError):  # pageable host cache
+        ops.decode_attn(q.to(gpu), kc, vc, bt.to(gpu), lens.to(gpu), 0.1, out, lse)
+    torch.cuda.synchronize()
+    assert torch.all(out == 7.0) and torch.all(lse == 7.0)
+
+
+@pytest.mark.parametrize("name", ["vicuna7b", "llama3_8b"])
+def test_full_size_workloads_match_oracle(gpu, name):
+    """Full headline shapes (n=128 MHA fp16 / n=256 GQA bf16), HBM tier in
+    vLLM's layout, fp32 out, against the float64 oracle on every row."""
+    w = cases.WORKLOADS[name]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    kc, vc, kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+    o, l = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out=out)
+    torch.cuda.synchronize()
+    kv_cpu = kv.cpu()
+    kc_c, vc_c = kv_cpu[..., : w.D], kv_cpu[..., w.D :]
+    ref_out, ref_lse, st = oracle.decode_attn_f64(q, kc_c, vc_c, oracle.VLLM_DIMS, bt, lens, w.scale)
+    assert st == 0
+    assert_out_close(o, ref_out, 2e-3)
+    assert_lse_close(l, ref_lse)

@@ -1,0 +1,265 @@
+// extern "C" entry points of libfdattn.so: argument validation on the host,
+// error reporting, pinned host memory, then the kernel launchers.
+//
+// Every check runs before any launch, so a rejected call writes nothing
+// (the contract of fastdecode/csrc/cpu_attn.cpp:433-477 and :495-510, where
+// TORCH_CHECK raises before the kernel runs).
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "fd_common.h"
+
+namespace fd {
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_error(hipError_t e, const char* what) {
+  return set_error(FD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+namespace {
+
+bool valid_dtype(int dt) { return dt == FD_F16 || dt == FD_BF16 || dt == FD_F32; }
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+}  // namespace
+}  // namespace fd
+
+using namespace fd;
+
+extern "C" {
+
+const char* fd_last_error(void) { return g_err; }
+
+int fd_abi_version(void) { return 1; }
+
+int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_size, int32_t block_size, int32_t bt_width,
+                                   size_t* bytes) {
+  if (bytes == nullptr) return set_error(FD_ERR_INVALID, "workspace_size: bytes is NULL");
+  if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
+      bt_width < 0)
+    return set_error(FD_ERR_INVALID, "workspace_size: bad sizes");
+  // The aligned fast path is the only one that needs workspace; size for it.
+  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
+                                   bt_width, FD_F16, true);
+  *bytes = decode_workspace_bytes(sp, n, num_heads, head_size);
+  return FD_OK;
+}
+
+int fd_paged_decode_partial(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                            const void* k_cache, const void* v_cache, int64_t kv_stride_block,
+                            int64_t kv_stride_head, int64_t kv_stride_token, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+                            const int32_t* lens, int32_t n, int32_t num_heads,
+                            int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                            float scale, int32_t kv_dtype, void* out, int64_t out_stride_seq,
+                            int64_t out_stride_head, int32_t out_dtype, float* lse,
+                            int64_t lse_stride_head, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (n < 0) return set_error(FD_ERR_INVALID, "decode: n must be >= 0 (got %d)", n);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return set_error(FD_ERR_INVALID,
+                     "decode: num_heads must be a multiple of num_kv_heads (%d, %d)", num_heads,
+                     num_kv_heads);
+  if (head_size <= 0 || head_size > 512)
+    return set_error(FD_ERR_UNSUPPORTED, "decode: head_size %d outside 1..512", head_size);
+  if (block_size <= 0) return set_error(FD_ERR_INVALID, "decode: block_size must be > 0");
+  if (bt_width < 0 || num_blocks < 0) return set_error(FD_ERR_INVALID, "decode: negative size");
+  if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "decode: unsupported kv dtype %d", kv_dtype);
+  if (out_dtype != kv_dtype && out_dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "decode: out dtype must equal the kv dtype or be fp32");
+  if (!std::isfinite(scale)) return set_error(FD_ERR_INVALID, "decode: scale is not finite");
+  if (n == 0) return FD_OK;
+  if (!q || !k_cache || !v_cache || !block_table || !lens || !out || !lse)
+    return set_error(FD_ERR_INVALID, "decode: NULL tensor pointer");
+  if (bt_width > 0 && bt_stride < bt_width)
+    return set_error(FD_ERR_INVALID, "decode: bt_stride %lld < bt_width %d",
+                     (long long)bt_stride, bt_width);
+
+  // An empty cache goes to the generic kernel, which never reads it.
+  const bool aligned = num_blocks > 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache) &&
+                       aligned16(out) && q_stride_seq % 8 == 0 && q_stride_head % 8 == 0 &&
+                       kv_stride_block % 8 == 0 && kv_stride_head % 8 == 0 &&
+                       kv_stride_token % 8 == 0 && out_stride_seq % 8 == 0 &&
+                       out_stride_head % 8 == 0 &&
+                       // one (block, head) run must be addressable by a 32-bit offset
+                       ((int64_t)(block_size - 1) * kv_stride_token + head_size) * 2 < (1ll << 31);
+  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
+                                   bt_width, kv_dtype, aligned);
+  const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+    return set_error(FD_ERR_WORKSPACE,
+                     "decode: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
+                     workspace == nullptr ? (size_t)0 : workspace_bytes);
+
+  DecodeArgs a{};
+  a.q = q;
+  a.q_ss = q_stride_seq;
+  a.q_sh = q_stride_head;
+  a.k = k_cache;
+  a.v = v_cache;
+  a.kv_sb = kv_stride_block;
+  a.kv_sh = kv_stride_head;
+  a.kv_st = kv_stride_token;
+  a.num_blocks = num_blocks;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.lens = lens;
+  a.n = n;
+  a.H = num_heads;
+  a.KVH = num_kv_heads;
+  a.D = head_size;
+  a.BS = block_size;
+  a.scale = scale;
+  a.kv_dtype = kv_dtype;
+  a.out = out;
+  a.out_ss = out_stride_seq;
+  a.out_sh = out_stride_head;
+  a.out_dtype = out_dtype;
+  a.lse = lse;
+  a.lse_sh = lse_stride_head;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return launch_decode(a, sp, static_cast<hipStream_t>(stream));
+}
+
+int fd_merge_attn_states(void* out, int64_t out_stride_seq, int64_t out_stride_head,
+                         int32_t out_dtype, const void* o_a, int64_t a_stride_seq,
+                         int64_t a_stride_head, int32_t a_dtype, const float* lse_a,
+                         int64_t lse_a_stride_head, const void* o_b, int64_t b_stride_seq,
+                         int64_t b_stride_head, int32_t b_dtype, const float* lse_b,
+                         int64_t lse_b_stride_head, float* out_lse,
+                         int64_t out_lse_stride_head, int32_t n, int32_t num_heads,
+                         int32_t head_size, void* stream) {
+  if (n < 0 || num_heads < 0 || head_size < 0)
+    return set_error(FD_ERR_INVALID, "merge: negative size");
+  if (!valid_dtype(out_dtype) || !valid_dtype(a_dtype) || !valid_dtype(b_dtype))
+    return set_error(FD_ERR_INVALID, "merge: unsupported dtype");
+  if ((int64_t)n * num_heads * head_size == 0) return FD_OK;
+  if (!out || !o_a || !lse_a || !o_b || !lse_b)
+    return set_error(FD_ERR_INVALID, "merge: NULL tensor pointer");
+  MergeArgs a{};
+  a.out = out;
+  a.out_ss = out_stride_seq;
+  a.out_sh = out_stride_head;
+  a.out_dt = out_dtype;
+  a.a = o_a;
+  a.a_ss = a_stride_seq;
+  a.a_sh = a_stride_head;
+  a.a_dt = a_dtype;
+  a.lse_a = lse_a;
+  a.lse_a_sh = lse_a_stride_head;
+  a.b = o_b;
+  a.b_ss = b_stride_seq;
+  a.b_sh = b_stride_head;
+  a.b_dt = b_dtype;
+  a.lse_b = lse_b;
+  a.lse_b_sh = lse_b_stride_head;
+  a.out_lse = out_lse;
+  a.out_lse_sh = out_lse_stride_head;
+  a.n = n;
+  a.H = num_heads;
+  a.D = head_size;
+  return launch_merge(a, static_cast<hipStream_t>(stream));
+}
+
+int fd_reshape_and_cache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                         const void* value, int64_t value_stride_tok,
+                         int64_t value_stride_head, void* k_cache, void* v_cache,
+                         int64_t cache_stride_block, int64_t cache_stride_token,
+                         int64_t cache_stride_head, int64_t num_blocks,
+                         const int64_t* slot_mapping, int32_t num_tokens,
+                         int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                         int32_t dtype, int32_t* error_count, void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
+      num_blocks < 0)
+    return set_error(FD_ERR_INVALID, "reshape_and_cache: bad sizes");
+  if (!valid_dtype(dtype)) return set_error(FD_ERR_INVALID, "reshape_and_cache: bad dtype");
+  if (num_tokens == 0) return FD_OK;
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping)
+    return set_error(FD_ERR_INVALID, "reshape_and_cache: NULL tensor pointer");
+  CacheWriteArgs a{};
+  a.key = key;
+  a.key_st = key_stride_tok;
+  a.key_sh = key_stride_head;
+  a.value = value;
+  a.value_st = value_stride_tok;
+  a.value_sh = value_stride_head;
+  a.kc = k_cache;
+  a.vc = v_cache;
+  a.c_sb = cache_stride_block;
+  a.c_st = cache_stride_token;
+  a.c_sh = cache_stride_head;
+  a.num_blocks = num_blocks;
+  a.slots = slot_mapping;
+  a.T = num_tokens;
+  a.KVH = num_kv_heads;
+  a.D = head_size;
+  a.BS = block_size;
+  a.elt = dtype_size(dtype);
+  a.err = error_count;
+  return launch_cache_write(a, static_cast<hipStream_t>(stream));
+}
+
+int fd_check_slots(const int64_t* slots, int64_t m, int64_t capacity, int64_t* first_bad) {
+  if (m < 0) return set_error(FD_ERR_INVALID, "check_slots: negative count");
+  if (m > 0 && slots == nullptr) return set_error(FD_ERR_INVALID, "check_slots: NULL slots");
+  for (int64_t j = 0; j < m; ++j) {
+    if (slots[j] < 0 || slots[j] >= capacity) {
+      if (first_bad) *first_bad = j;
+      return set_error(FD_ERR_RANGE, "host-tier slot out of range: %lld (capacity %lld)",
+                       (long long)slots[j], (long long)capacity);
+    }
+  }
+  return FD_OK;
+}
+
+int fd_host_alloc(size_t bytes, void** host_ptr) {
+  if (host_ptr == nullptr) return set_error(FD_ERR_INVALID, "host_alloc: host_ptr is NULL");
+  *host_ptr = nullptr;
+  if (bytes == 0) bytes = 16;
+  unsigned flags = hipHostMallocMapped | hipHostMallocPortable;
+  const char* nc = getenv("FD_HOST_NONCOHERENT");
+  if (nc != nullptr && nc[0] == '1') flags |= hipHostMallocNonCoherent;
+  const hipError_t e = hipHostMalloc(host_ptr, bytes, flags);
+  if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
+  return FD_OK;
+}
+
+int fd_host_free(void* host_ptr) {
+  if (host_ptr == nullptr) return FD_OK;
+  const hipError_t e = hipHostFree(host_ptr);
+  return e == hipSuccess ? FD_OK : hip_error(e, "hipHostFree");
+}
+
+int fd_host_device_pointer(void* host_ptr, void** device_ptr) {
+  if (host_ptr == nullptr || device_ptr == nullptr)
+    return set_error(FD_ERR_INVALID, "host_device_pointer: NULL argument");
+  const hipError_t e = hipHostGetDevicePointer(device_ptr, host_ptr, 0);
+  return e == hipSuccess ? FD_OK : hip_error(e, "hipHostGetDevicePointer");
+}
+
+int fd_stream_copy(void* dst, const void* src, size_t bytes, void* stream) {
+  if (bytes % 16 != 0) return set_error(FD_ERR_INVALID, "stream_copy: bytes %% 16 != 0");
+  if (bytes == 0) return FD_OK;
+  if (!dst || !src || !aligned16(dst) || !aligned16(src))
+    return set_error(FD_ERR_INVALID, "stream_copy: NULL or unaligned pointer");
+  return launch_stream_copy(dst, src, bytes, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,221 @@
+// Shared helpers for the gfx950 split decode-attention kernels: element
+// conversions, 64-lane wavefront reductions, error reporting and launch
+// bookkeeping used by every translation unit of libfdattn.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fdattn.h"
+
+namespace fd {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- errors
+// Records a printf-style message for fd_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Converts a failed HIP call into FD_ERR_HIP with the runtime's message.
+int hip_error(hipError_t e, const char* what);
+
+inline int dtype_size(int dt) {
+  return dt == FD_F32 ? 4 : (dt == FD_F16 || dt == FD_BF16) ? 2 : 0;
+}
+
+// ---------------------------------------------------------------- types
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+
+// Storage tags for 16-bit KV elements. Both are moved around as raw 16-bit
+// words; only the arithmetic below differs.
+struct F16 {
+  static constexpr int kCode = FD_F16;
+};
+struct BF16 {
+  static constexpr int kCode = FD_BF16;
+};
+
+// Low / high 16-bit element of a packed 32-bit word as fp32.
+__device__ __forceinline__ float lo_f32(F16, uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).x;
+}
+__device__ __forceinline__ float hi_f32(F16, uint32_t w) {
+  return (float)__builtin_bit_cast(half2_t, w).y;
+}
+__device__ __forceinline__ float lo_f32(BF16, uint32_t w) {
+  return __uint_as_float(w << 16);
+}
+__device__ __forceinline__ float hi_f32(BF16, uint32_t w) {
+  return __uint_as_float(w & 0xffff0000u);
+}
+
+// acc + a.lo*b.lo + a.hi*b.hi with fp32 accumulation (v_dot2_f32_{f16,bf16}).
+__device__ __forceinline__ float dot2(F16, uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, a),
+                                __builtin_bit_cast(half2_t, b), acc, false);
+}
+__device__ __forceinline__ float dot2(BF16, uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf162_t, a),
+                                         __builtin_bit_cast(bf162_t, b), acc,
+                                         false);
+}
+
+// fp32 -> 16-bit storage, round to nearest even.
+__device__ __forceinline__ uint16_t from_f32(F16, float x) {
+  return __builtin_bit_cast(uint16_t, (_Float16)x);
+}
+__device__ __forceinline__ uint16_t from_f32(BF16, float x) {
+  return __builtin_bit_cast(uint16_t, (__bf16)x);
+}
+
+// Generic scalar load/store by runtime dtype (used by the slow paths).
+__device__ __forceinline__ float load_elem(const void* p, int64_t i, int dt) {
+  if (dt == FD_F32) return static_cast<const float*>(p)[i];
+  const uint16_t w = static_cast<const uint16_t*>(p)[i];
+  return dt == FD_F16 ? (float)__builtin_bit_cast(_Float16, w)
+                      : __uint_as_float(static_cast<uint32_t>(w) << 16);
+}
+__device__ __forceinline__ void store_elem(void* p, int64_t i, int dt, float x) {
+  if (dt == FD_F32) {
+    static_cast<float*>(p)[i] = x;
+  } else if (dt == FD_F16) {
+    static_cast<uint16_t*>(p)[i] = from_f32(F16{}, x);
+  } else {
+    static_cast<uint16_t*>(p)[i] = from_f32(BF16{}, x);
+  }
+}
+
+// ---------------------------------------------------------------- DPP
+// DPP control words (GCN/CDNA "data parallel primitives" operand modifiers).
+constexpr int kDppQuadXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;   // lane i <- lane 7-i in each 8
+constexpr int kDppRowMirror = 0x140;       // lane i <- lane 15-i in each 16
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl,
+                                         0xF, 0xF, false));
+}
+
+// Sum over aligned groups of kLanes consecutive lanes (4, 8, 16 or 32); every
+// lane of a group receives the group's sum. The butterfly uses quad
+// permutes and row mirrors, so each step is one v_add_f32 with a DPP operand;
+// the 32-lane step crosses DPP rows with a ds_swizzle.
+template <int kLanes>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(kLanes == 4 || kLanes == 8 || kLanes == 16 || kLanes == 32,
+                "group_sum: unsupported group");
+  x += dpp<kDppQuadXor1>(x);
+  x += dpp<kDppQuadXor2>(x);
+  if constexpr (kLanes >= 8) x += dpp<kDppRowHalfMirror>(x);
+  if constexpr (kLanes >= 16) x += dpp<kDppRowMirror>(x);
+  if constexpr (kLanes >= 32) {
+    // swizzle bitmask mode: and_mask=0x1f, or_mask=0, xor_mask=0x10
+    x += __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F));
+  }
+  return x;
+}
+
+__device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
+  return __shfl_xor(x, mask, kWave);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += shfl_xor_f32(x, m);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, shfl_xor_f32(x, m));
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
+__device__ __forceinline__ float qnan() { return __builtin_nanf(""); }
+
+// ---------------------------------------------------------------- launchers
+// Implemented in decode_partial.hip / merge.hip / cache_write.hip; the C ABI
+// in capi.hip validates arguments and then calls these.
+struct DecodeArgs {
+  const void* q;
+  int64_t q_ss, q_sh;
+  const void* k;
+  const void* v;
+  int64_t kv_sb, kv_sh, kv_st;
+  int64_t num_blocks;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int32_t bt_width;
+  const int32_t* lens;
+  int32_t n, H, KVH, D, BS;
+  float scale;
+  int32_t kv_dtype;
+  void* out;
+  int64_t out_ss, out_sh;
+  int32_t out_dtype;
+  float* lse;
+  int64_t lse_sh;
+  void* workspace;
+  size_t workspace_bytes;
+};
+
+// Split plan of one decode call: blocks per split and the split count.
+struct SplitPlan {
+  int32_t split_blocks;  // blocks handled by one wavefront task
+  int32_t max_splits;    // ceil(bt_width / split_blocks)
+  bool fast;             // the tiled kernel applies (else the generic one)
+};
+
+SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
+                      int32_t bt_width, int32_t kv_dtype, bool aligned);
+size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H,
+                              int32_t D);
+int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s);
+
+struct MergeArgs {
+  void* out;
+  int64_t out_ss, out_sh;
+  int32_t out_dt;
+  const void* a;
+  int64_t a_ss, a_sh;
+  int32_t a_dt;
+  const float* lse_a;
+  int64_t lse_a_sh;
+  const void* b;
+  int64_t b_ss, b_sh;
+  int32_t b_dt;
+  const float* lse_b;
+  int64_t lse_b_sh;
+  float* out_lse;
+  int64_t out_lse_sh;
+  int32_t n, H, D;
+};
+int launch_merge(const MergeArgs& a, hipStream_t s);
+
+struct CacheWriteArgs {
+  const void* key;
+  int64_t key_st, key_sh;
+  const void* value;
+  int64_t value_st, value_sh;
+  void* kc;
+  void* vc;
+  int64_t c_sb, c_st, c_sh;
+  int64_t num_blocks;
+  const int64_t* slots;
+  int32_t T, KVH, D, BS;
+  int32_t elt;  // element size in bytes
+  int32_t* err;
+};
+int launch_cache_write(const CacheWriteArgs& a, hipStream_t s);
+
+int launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+}  // namespace fd

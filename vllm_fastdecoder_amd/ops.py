@@ -1,0 +1,318 @@
+"""Torch-facing wrappers of the HIP kernels, with the reference's signatures.
+
+Reference surfaces this mirrors:
+  * the CPU extension loaded by fastdecode/cpu_ops.py:21-46 and defined in
+    fastdecode/csrc/cpu_attn.cpp:452-537 -- `decode_attn` and `store_kv`;
+  * the GPU primitives behind backend.OPS (fastdecode/backend.py:42-64) --
+    FlashAttention's paged decode partial, `reshape_and_cache_flash` and
+    `merge_attn_states`.
+
+Every function launches on the current HIP stream of the output's device and
+returns without synchronising. Argument checks mirror the reference's
+TORCH_CHECKs and raise RuntimeError before anything is written. Host-tier
+caches must be pinned (see pinned.py); the kernels read them in place.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+from .pinned import device_ptr
+
+_DT = {torch.float16: _lib.FD_F16, torch.bfloat16: _lib.FD_BF16, torch.float32: _lib.FD_F32}
+
+
+def _dtype_code(t: torch.Tensor, what: str) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise RuntimeError(f"{what}: unsupported dtype {t.dtype}") from None
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _stream_for(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_device(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    """Small index tensors given on the host are copied to the device."""
+    if t.is_cuda:
+        return t
+    return t.to(device, non_blocking=False)
+
+
+class _Workspace:
+    """Grow-only device scratch per device for the split partials (the same
+    grow-only policy as the reference's PinnedStaging.get, state.py:115-124)."""
+
+    def __init__(self) -> None:
+        self._bufs: dict[int, torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        with self._lock:
+            buf = self._bufs.get(idx)
+            if buf is None or buf.numel() < nbytes:
+                cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
+                buf = torch.empty(cap, dtype=torch.uint8, device=torch.device("cuda", idx))
+                self._bufs[idx] = buf
+            return buf
+
+
+WORKSPACE = _Workspace()
+
+
+def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
+    size = ctypes.c_size_t()
+    _lib.check(_lib.load_lib().fd_paged_decode_workspace_size(n, H, KVH, D, BS, width, ctypes.byref(size)))
+    return int(size.value)
+
+
+def paged_decode_partial(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    kv_strides: tuple[int, int, int],
+    num_blocks: int,
+    block_size: int,
+    num_kv_heads: int,
+    block_table: torch.Tensor,
+    lens: torch.Tensor,
+    scale: float,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    workspace: torch.Tensor | None = None,
+) -> None:
+    """Layout-generic entry: kv_strides = (block, head, token) in elements."""
+    _require(q.is_cuda and out.is_cuda and lse.is_cuda, "q, out and lse must be on the GPU")
+    _require(q.dim() == 3 and out.shape == q.shape, "q and out must be [n, H, D] of one shape")
+    n, H, D = q.shape
+    _require(q.stride(2) == 1 and out.stride(2) == 1, "head_size must be the contiguous dim")
+    _require(lse.dtype == torch.float32 and lse.dim() == 2 and tuple(lse.shape) == (H, n),
+             "lse must be float32 [H, n]")
+    _require(n == 0 or lse.stride(1) == 1, "lse rows must be contiguous")
+    _require(block_table.dtype == torch.int32 and lens.dtype == torch.int32,
+             "block_table and lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == n and lens.shape == (n,),
+             "block_table must be [n, W] and lens [n]")
+    kv_dt = _dtype_code(k_cache, "k_cache")
+    _require(q.dtype == k_cache.dtype and v_cache.dtype == k_cache.dtype,
+             "q, k_cache and v_cache must share a dtype")
+    _require(out.dtype == q.dtype or out.dtype == torch.float32, "out must be q's dtype or float32")
+    _require(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape,
+             "k_cache and v_cache must share shape and strides")
+    if n == 0:
+        return
+    dev = q.device
+    bt = _on_device(block_table, dev)
+    ln = _on_device(lens, dev)
+    _require(bt.stride(1) == 1, "block_table rows must be contiguous")
+    ln = ln.contiguous()
+    W = bt.shape[1]
+    need = workspace_bytes(n, H, num_kv_heads, D, block_size, W)
+    if workspace is None:
+        workspace = WORKSPACE.get(dev, need)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    lib = _lib.load_lib()
+    _lib.check(
+        lib.fd_paged_decode_partial(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            device_ptr(k_cache), device_ptr(v_cache),
+            kv_strides[0], kv_strides[1], kv_strides[2],
+            num_blocks,
+            bt.data_ptr(), bt.stride(0), W,
+            ln.data_ptr(),
+            n, H, num_kv_heads, D,
+            block_size, float(scale), kv_dt,
+            out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
+            lse.data_ptr(), lse.stride(0),
+            ws_ptr, ws_len,
+            _stream_for(q),
+        )
+    )
+
+
+def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse) -> None:
+    """Host-tier layout partial, signature of cpu_attn.cpp:456-489.
+
+    q [n, H, D]; k_cache/v_cache [C, KVH, BS, D] (pinned host memory or HBM);
+    block_table [n, W] int32 (tier-relative ids in sequence order); lens [n]
+    int32; out [n, H, D] (q's dtype, or float32); lse [H, n] float32.
+    """
+    _require(k_cache.dim() == 4 and v_cache.shape == k_cache.shape,
+             "k_cache/v_cache must be [C, KVH, BS, D]")
+    C, KVH, BS, D = k_cache.shape
+    _require(q.dim() == 3 and q.shape[2] == D, "head size mismatch")
+    _require(q.shape[1] % KVH == 0, "num_heads must be a multiple of num_kv_heads")
+    _require(k_cache.stride(3) == 1, "k_cache must be contiguous in head_size")
+    paged_decode_partial(
+        q, k_cache, v_cache, (k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)),
+        C, BS, KVH, block_table, lens, scale, out, lse,
+    )
+
+
+def paged_decode(
+    q: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seqused_k: torch.Tensor,
+    softmax_scale: float,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """HBM-tier partial in vLLM's paged layout: the decode call of
+    flash_attn_varlen_func at fastdecode/backend.py:306-314 (one query token
+    per row, block_table + seqused_k, return_softmax_lse=True).
+
+    key_cache/value_cache [B, BS, KVH, D] (e.g. the K and V halves of the
+    interleaved [B, BS, KVH, 2D] cache). Returns out [n, H, D] (q's dtype
+    unless `out` is given) and lse [H, n] float32. Rows with seqused_k == 0
+    give out = 0 and lse = -inf (no FA row filtering is needed).
+    """
+    _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape,
+             "key_cache/value_cache must be [B, BS, KVH, D]")
+    B, BS, KVH, D = key_cache.shape
+    n, H = q.shape[0], q.shape[1]
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty(H, n, dtype=torch.float32, device=q.device)
+    _require(key_cache.stride(3) == 1, "key_cache must be contiguous in head_size")
+    paged_decode_partial(
+        q, key_cache, value_cache,
+        (key_cache.stride(0), key_cache.stride(2), key_cache.stride(1)),
+        B, BS, KVH, block_table, seqused_k, softmax_scale, out, lse,
+    )
+    return out, lse
+
+
+def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
+    """out = LSE-merge of two partials; vLLM merge_attn_states signature as
+    used at fastdecode/backend.py:53-55 (rule of cpu_ops.py:93-113)."""
+    _require(out.dim() == 3 and o_a.shape == out.shape and o_b.shape == out.shape,
+             "out, o_a, o_b must be [n, H, D] of one shape")
+    n, H, D = out.shape
+    for t, name in ((out, "out"), (o_a, "o_a"), (o_b, "o_b")):
+        _require(t.is_cuda and t.stride(2) == 1, f"{name} must be a GPU tensor contiguous in D")
+    for t, name in ((lse_a, "lse_a"), (lse_b, "lse_b")):
+        _require(t.is_cuda and t.dtype == torch.float32 and tuple(t.shape) == (H, n),
+                 f"{name} must be float32 [H, n] on the GPU")
+        _require(n == 0 or t.stride(1) == 1, f"{name} rows must be contiguous")
+    if out_lse is not None:
+        _require(out_lse.dtype == torch.float32 and tuple(out_lse.shape) == (H, n) and
+                 (n == 0 or out_lse.stride(1) == 1), "out_lse must be float32 [H, n]")
+    _lib.check(
+        _lib.load_lib().fd_merge_attn_states(
+            out.data_ptr(), out.stride(0), out.stride(1), _dtype_code(out, "out"),
+            o_a.data_ptr(), o_a.stride(0), o_a.stride(1), _dtype_code(o_a, "o_a"),
+            lse_a.data_ptr(), lse_a.stride(0),
+            o_b.data_ptr(), o_b.stride(0), o_b.stride(1), _dtype_code(o_b, "o_b"),
+            lse_b.data_ptr(), lse_b.stride(0),
+            out_lse.data_ptr() if out_lse is not None else None,
+            out_lse.stride(0) if out_lse is not None else 0,
+            n, H, D,
+            _stream_for(out),
+        )
+    )
+
+
+def _cache_write(key, value, k_cache, v_cache, strides_btg, num_blocks, block_size,
+                 slot_mapping, error_count) -> None:
+    _require(key.dim() == 3 and value.shape == key.shape, "key/value must be [T, KVH, D]")
+    T, KVH, D = key.shape
+    _require(key.stride(2) == 1 and value.stride(2) == 1, "key/value must be contiguous in D")
+    _require(key.dtype == k_cache.dtype and value.dtype == key.dtype and v_cache.dtype == key.dtype,
+             "key, value and caches must share a dtype")
+    _require(slot_mapping.dtype == torch.int64 and slot_mapping.dim() == 1
+             and slot_mapping.shape[0] >= T, "slot_mapping must be int64 [>= T]")
+    if T == 0:
+        return
+    _require(key.is_cuda and value.is_cuda, "key/value must be on the GPU")
+    slots = _on_device(slot_mapping, key.device).contiguous()
+    err_ptr = None
+    if error_count is not None:
+        _require(error_count.is_cuda and error_count.dtype == torch.int32, "error_count: int32 GPU")
+        err_ptr = error_count.data_ptr()
+    _lib.check(
+        _lib.load_lib().fd_reshape_and_cache(
+            key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1),
+            device_ptr(k_cache), device_ptr(v_cache),
+            strides_btg[0], strides_btg[1], strides_btg[2],
+            num_blocks,
+            slots.data_ptr(), T,
+            KVH, D, block_size,
+            _dtype_code(key, "key"), err_ptr,
+            _stream_for(key),
+        )
+    )
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
+                      kv_cache_dtype: str = "auto", k_scale=None, v_scale=None,
+                      error_count: torch.Tensor | None = None) -> None:
+    """vLLM reshape_and_cache_flash signature (fastdecode/backend.py:270-273):
+    key_cache/value_cache [B, BS, KVH, D] views; slots < 0 are skipped.
+    Only the unquantised cache ("auto"/fp16/bf16) is supported, as in the
+    reference backend (fastdecode/backend.py:68,211-212)."""
+    _require(kv_cache_dtype in ("auto", "float16", "bfloat16", "fp16", "bf16"),
+             f"quantized KV cache ({kv_cache_dtype}) is not supported")
+    _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape
+             and key_cache.stride() == value_cache.stride(), "caches must be [B, BS, KVH, D]")
+    B, BS, KVH, D = key_cache.shape
+    _require(key.shape[1] == KVH and key.shape[2] == D, "key shape does not match the cache")
+    _cache_write(key, value, key_cache, value_cache,
+                 (key_cache.stride(0), key_cache.stride(1), key_cache.stride(2)),
+                 B, BS, slot_mapping[: key.shape[0]], error_count)
+
+
+def store_kv(k, v, slots, k_cache, v_cache) -> None:
+    """Host-tier KV write, signature of cpu_attn.cpp:492-517.
+
+    k, v [m, KVH, D]; slots [m] int64 (tier-relative); k_cache/v_cache
+    [C, KVH, BS, D] pinned host memory (or HBM). Every slot is range-checked
+    before anything is written; an out-of-range slot raises RuntimeError.
+    """
+    _require(k_cache.dim() == 4 and v_cache.shape == k_cache.shape
+             and k_cache.stride() == v_cache.stride(), "caches must be [C, KVH, BS, D]")
+    C, KVH, BS, D = k_cache.shape
+    _require(slots.dtype == torch.int64, "slots must be int64")
+    m = k.shape[0]
+    if m == 0:
+        return
+    _require(k.dim() == 3 and k.shape[1] == KVH and k.shape[2] == D and v.shape == k.shape,
+             "k/v must be [m, KVH, D] matching the cache")
+    cap = C * BS
+    if slots.is_cuda:
+        bad = int(((slots[:m] < 0) | (slots[:m] >= cap)).sum())  # synchronises
+        _require(bad == 0, f"host-tier slot out of range (capacity {cap})")
+    else:
+        host = slots[:m].contiguous()
+        first = ctypes.c_int64(-1)
+        _lib.check(_lib.load_lib().fd_check_slots(host.data_ptr(), m, cap, ctypes.byref(first)))
+    dev = k.device if k.is_cuda else torch.device("cuda", torch.cuda.current_device())
+    kk = _on_device(k, dev)
+    vv = _on_device(v, dev)
+    _cache_write(kk, vv, k_cache, v_cache,
+                 (k_cache.stride(0), k_cache.stride(2), k_cache.stride(1)),
+                 C, BS, slots[:m], None)
+
+
+def stream_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """Byte copy with the attention kernels' 16-byte loads (measurement aid)."""
+    nbytes = src.numel() * src.element_size()
+    _require(dst.numel() * dst.element_size() >= nbytes, "dst too small")
+    _lib.check(_lib.load_lib().fd_stream_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream_for(src)))
