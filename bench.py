@@ -1,0 +1,347 @@
+#!/usr/bin/env python3
+"""Split decode-attention benchmark on one MI355X.
+
+Default workload (vicuna-7b decode-attention shape, one layer):
+  n = 128 sequences, 32 query / 32 kv heads, head_size 128, block_size 16,
+  fp16 KV ~ N(0,1), context lengths ~ U[256, 2048], pool = the rows' blocks,
+  every block in HBM in vLLM's [B, BS, KVH, 2D] layout.
+A step is one paged partial decode over every row's blocks (the HBM-tier
+FlashAttention call of the reference, fastdecode/backend.py:305-316), with the
+inputs resident in HBM before the timed region starts.
+
+Printed (one JSON line):
+  value        algorithmic bytes per step / step time, GB/s (HBM)
+  roofline     the decode kernel against MI355X's 8 TB/s HBM peak
+  cpu_baseline the reference's own cpu_attn.cpp kernel (built from its
+               source into oracle/_ref) on this host's cores, same shape,
+               host-tier layout; the restated C kernel when that build is
+               absent
+  tokens_per_s n / (t_layer * 32 layers), the reference's formula
+               (scripts/probe_cpu_attn.py:63-68)
+  split_run    the same batch with 60% of each row's blocks (its last ones)
+               in pinned host memory read zero-copy over the link: HBM
+               partial + host partial + merge, with the link rate
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBPS = 8000.0
+LAYERS = 32
+METRIC = "split decode-attn achieved HBM GB/s (% of peak) + tokens/s, vicuna-7b shape"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="vicuna7b", choices=["vicuna7b", "llama3_8b", "correctness"])
+    ap.add_argument("--layout", default="vllm", choices=["vllm", "host"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-split-run", action="store_true")
+    ap.add_argument("--cpu-iters", type=int, default=20)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run the 16-byte stream-copy kernel over MIB MiB (counter calibration)")
+    return ap.parse_args()
+
+
+def copy_calibration(mib: int, steps: int, warmup: int) -> int:
+    """Known-size copy with the library's stream-copy kernel: the reference
+    point that scales the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    from vllm_fastdecoder_amd import ops
+
+    dev = torch.device("cuda", 0)
+    src = torch.ones(mib << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    ms = time_gpu(lambda: ops.stream_copy(dst, src), steps, warmup, torch.cuda.current_stream(dev))
+    print(json.dumps({"copy_bytes_read": mib << 20, "copy_bytes_written": mib << 20,
+                      "ms": round(ms, 4), "GBps_rw": round(2 * (mib << 20) / (ms / 1e3) / 1e9, 1)}))
+    return 0
+
+
+def algorithmic_bytes(lens, n, H, KVH, D, BS, elt, out_elt):
+    """Bytes one partial must move (per the path's roofline accounting):
+    K and V once per context token, q, out, lse, the table entries used and
+    the lengths."""
+    import torch
+
+    L = lens.clamp(min=0).to(torch.int64)
+    nb = (L + BS - 1) // BS
+    kv = int(L.sum()) * 2 * KVH * D * elt
+    return kv + n * H * D * elt + n * H * D * out_elt + 4 * n * H + 4 * int(nb.sum()) + 4 * n, kv
+
+
+def time_gpu(fn, steps, warmup, stream):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms
+
+
+def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
+    """The reference CPU kernel on this host's cores, same seeded workload in
+    the reference's host-tier layout [C, KVH, BS, D]."""
+    import torch
+
+    import oracle
+    from tests import cases
+
+    cores = len(os.sched_getaffinity(0))
+    k, v, _ = cases.kv_pool(w, pool, "host", "cuda")
+    k = k.cpu()
+    v = v.cpu()
+    torch.cuda.synchronize()
+    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32)
+    ext = oracle.ref_ext()
+    if ext is not None:
+        ext.set_num_threads(cores)
+        kind = "reference"
+
+        def call():
+            ext.decode_attn(q_cpu, k, v, bt, lens, w.scale, out, lse)
+    else:
+        kind = "port"
+        out32 = torch.empty(w.n, w.H, w.D, dtype=torch.float32)
+
+        def call():
+            oracle.decode_attn_cpu_f32(q_cpu, k, v, bt, lens, w.scale, out32, lse, threads=cores)
+    for _ in range(3):
+        call()
+    times = []
+    t_budget = time.perf_counter() + 30.0
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        call()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() > t_budget:
+            break
+    times.sort()
+    t = times[len(times) // 2]
+    _, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    del k, v
+    return {
+        "value": round(kvb / t / 1e9, 2),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": (f"full {w.name} workload (n={w.n}, {w.H}/{w.KVH} heads, D={w.D}, "
+                   f"{str(w.dtype).replace('torch.', '')}) in the host-tier layout; K+V bytes / "
+                   f"median of {len(times)} calls after 3 warm-ups; "
+                   + ("fastdecode/csrc/cpu_attn.cpp decode_attn built from source"
+                      if kind == "reference" else "restated fp32 two-pass C kernel")),
+        "ms_per_call": round(t * 1e3, 3),
+        "tokens_per_s": round(w.n / (t * LAYERS), 1),
+    }
+
+
+def split_run(w, lens, bt, q, steps, warmup, stream):
+    """60% of each row's blocks (the last ones) in pinned host memory, the rest
+    in HBM: HBM partial + host partial (zero-copy) + LSE merge."""
+    import torch
+
+    from tests import cases
+    from vllm_fastdecoder_amd import ops
+    from vllm_fastdecoder_amd.pinned import pinned_empty
+
+    dev = q.device
+    nb = (lens + w.BS - 1) // w.BS
+    n_host = torch.ceil(nb.double() * 0.6).to(torch.int32)
+    n_hbm = nb - n_host
+    last = lens - (nb - 1) * w.BS
+    W = bt.shape[1]
+    bt_g = torch.zeros(w.n, W, dtype=torch.int32)
+    bt_c = torch.zeros(w.n, W, dtype=torch.int32)
+    len_g = (n_hbm * w.BS).to(torch.int32)
+    len_c = (lens - len_g).to(torch.int32)
+    G = int(n_hbm.sum())
+    C = int(n_host.sum())
+    pg = pc = 0
+    for i in range(w.n):
+        a, b = int(n_hbm[i]), int(n_host[i])
+        bt_g[i, :a] = torch.arange(pg, pg + a, dtype=torch.int32)
+        bt_c[i, :b] = torch.arange(pc, pc + b, dtype=torch.int32)
+        pg += a
+        pc += b
+    del last
+    kc_g, vc_g, kv = cases.kv_pool(w, max(G, 1), "vllm", dev)
+    hk = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
+    hv = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
+    # fill the host tier in slabs (N(0,1), seeded)
+    gen = torch.Generator(device=dev).manual_seed(4242)
+    slab = 2048
+    for t in (hk, hv):
+        for s in range(0, C, slab):
+            e = min(C, s + slab)
+            t[s:e].copy_(torch.randn(e - s, w.KVH, w.BS, w.D, generator=gen, device=dev).to(w.dtype).cpu())
+    bt_g_d, bt_c_d = bt_g.to(dev), bt_c.to(dev)
+    len_g_d, len_c_d = len_g.to(dev), len_c.to(dev)
+    o_g = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
+    l_g = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
+    o_c = torch.empty_like(o_g)
+    l_c = torch.empty_like(l_g)
+    merged = torch.empty_like(o_g)
+
+    def hbm():
+        ops.paged_decode(q, kc_g, vc_g, bt_g_d, len_g_d, w.scale, out=o_g, lse=l_g)
+
+    def host():
+        ops.decode_attn(q, hk, hv, bt_c_d, len_c_d, w.scale, o_c, l_c)
+
+    def merge():
+        ops.merge_attn_states(merged, o_g, l_g, o_c, l_c)
+
+    def step():
+        hbm()
+        host()
+        merge()
+
+    host_steps = max(2, min(steps, 5))
+    t_hbm = time_gpu(hbm, steps, warmup, stream)
+    t_host = time_gpu(host, host_steps, 1, stream)
+    t_merge = time_gpu(merge, steps, warmup, stream)
+    t_step = time_gpu(step, host_steps, 1, stream)
+    b_hbm, kv_hbm = algorithmic_bytes(len_g, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    b_host, kv_host = algorithmic_bytes(len_c, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    del kv, hk, hv
+    return {
+        "host_fraction_blocks": 0.6,
+        "hbm_partial_ms": round(t_hbm, 4),
+        "hbm_partial_GBps": round(b_hbm / (t_hbm / 1e3) / 1e9, 1),
+        "host_partial_ms": round(t_host, 3),
+        "host_link_GBps": round(kv_host / (t_host / 1e3) / 1e9, 2),
+        "merge_ms": round(t_merge, 4),
+        "step_ms": round(t_step, 3),
+        "step_tokens_per_s": round(w.n / (t_step / 1e3 * LAYERS), 1),
+        "note": "host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not `value`",
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        return 2
+    import torch
+
+    from tests import cases
+    from vllm_fastdecoder_amd import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration, args.steps, args.warmup)
+    w = cases.WORKLOADS[args.workload]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    if args.layout == "vllm":
+        kc, vc, _keep = cases.kv_pool(w, pool, "vllm", dev)
+    else:
+        kc, vc, _keep = cases.kv_pool(w, pool, "host", dev)
+    q = cases.queries(w, dev)
+    bt_d, lens_d = bt.to(dev), lens.to(dev)
+    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    if args.layout == "vllm":
+        def step():
+            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse)
+    else:
+        def step():
+            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse)
+
+    elt = 2
+    nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, elt, elt)
+    ms = time_gpu(step, args.steps, args.warmup, stream)
+    gbps = nbytes / (ms / 1e3) / 1e9
+
+    # HBM bytes per launch from the committed counter runs, used only while
+    # they describe this exact kernel source
+    traffic = None
+    prof = ROOT / "profiles" / f"traffic_{w.name}_{args.layout}.json"
+    if prof.exists():
+        import hashlib
+
+        src = ROOT / "vllm_fastdecoder_amd" / "csrc" / "decode_partial.hip"
+        sha = hashlib.sha256(src.read_bytes()).hexdigest()[:16]
+        try:
+            rec = json.loads(prof.read_text())
+            if rec.get("source_sha256_16") == sha:
+                traffic = rec.get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16" if w.dtype == torch.float16 else "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{w.name} decode attention, one layer: n={w.n}, {w.H}/{w.KVH} heads, "
+                         f"D={w.D}, BS={w.BS}, L~U[{w.lo},{w.hi}], all blocks in HBM "
+                         f"({'vLLM [B,BS,KVH,2D]' if args.layout == 'vllm' else 'host [C,KVH,BS,D]'} layout)"),
+            "global_batch": w.n,
+            "seq_len": w.hi,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": nbytes,
+            "kernel_ms": round(ms, 5),
+        },
+        "tokens_per_s": round(w.n / (ms / 1e3 * LAYERS), 1),
+        "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "kv_bytes_per_step": kvb,
+    }
+    del _keep, kc, vc
+    torch.cuda.empty_cache()
+    if not args.no_split_run and w.name == "vicuna7b":
+        result["split_run"] = split_run(w, lens, bt, q, args.steps, args.warmup, stream)
+        torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, lens, bt, pool, q.cpu(), args.cpu_iters)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -125,6 +125,19 @@ def queries(w: Workload, device) -> torch.Tensor:
     return torch.randn(w.n, w.H, w.D, generator=g).to(w.dtype).to(device)
 
 
+def tensor_digest(*tensors: torch.Tensor) -> str:
+    """sha256 over the raw bytes of CPU tensors (detects generator drift)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for t in tensors:
+        t = t.detach().cpu().contiguous()
+        h.update(str(t.dtype).encode())
+        h.update(str(tuple(t.shape)).encode())
+        h.update(t.view(torch.uint8).numpy().tobytes() if t.numel() else b"")
+    return h.hexdigest()
+
+
 def kv_bytes(lens: torch.Tensor, KVH: int, D: int, elt: int) -> int:
     """Algorithmic K+V bytes of one partial: 2 * KVH * D * elt per token."""
     return int(lens.clamp(min=0).sum()) * 2 * KVH * D * elt

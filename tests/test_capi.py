@@ -1,0 +1,114 @@
+"""CPU checks of the C ABI (no GPU compute): the library loads, exports every
+function include/fdattn.h declares, and its host-side argument validation
+rejects bad calls before any launch (the TORCH_CHECK contract of
+fastdecode/csrc/cpu_attn.cpp:433-477 and the slot rule of :506-510)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from vllm_fastdecoder_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fdattn.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(fd_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_bound_signatures():
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load_lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.fd_abi_version() == _lib.ABI_VERSION
+
+
+def test_check_slots_host_rule():
+    lib = _lib.load_lib()
+    good = (ctypes.c_int64 * 4)(0, 5, 31, 17)
+    assert lib.fd_check_slots(good, 4, 32, None) == _lib.FD_OK
+    bad = (ctypes.c_int64 * 4)(0, 5, 32, 17)
+    first = ctypes.c_int64(-1)
+    assert lib.fd_check_slots(bad, 4, 32, ctypes.byref(first)) == _lib.FD_ERR_RANGE
+    assert first.value == 2
+    assert b"out of range" in lib.fd_last_error()
+    neg = (ctypes.c_int64 * 1)(-1)
+    assert lib.fd_check_slots(neg, 1, 32, None) == _lib.FD_ERR_RANGE
+
+
+def test_workspace_size_query():
+    lib = _lib.load_lib()
+    size = ctypes.c_size_t()
+    # vicuna-7b shape: 128 sequences, 32/32 heads, width 128 blocks
+    assert lib.fd_paged_decode_workspace_size(128, 32, 32, 128, 16, 128, ctypes.byref(size)) == 0
+    assert size.value > 0
+    # a head size the tiled kernel does not take needs no workspace
+    assert lib.fd_paged_decode_workspace_size(7, 8, 8, 72, 16, 6, ctypes.byref(size)) == 0
+    assert size.value == 0
+    assert lib.fd_paged_decode_workspace_size(-1, 8, 8, 64, 16, 6, ctypes.byref(size)) != 0
+
+
+def _decode(lib, **over):
+    """fd_paged_decode_partial with plausible pointers (never dereferenced:
+    every call here must be rejected by host validation)."""
+    a = dict(q=16, qss=8 * 64, qsh=64, k=32, v=48, sb=4 * 16 * 64, sh=16 * 64, st=64, nblk=10,
+             bt=64, bts=4, btw=4, lens=80, n=2, H=8, KVH=4, D=64, BS=16, scale=0.125, dt=0,
+             out=96, oss=8 * 64, osh=64, odt=0, lse=112, lsh=2, ws=None, wsb=0)
+    a.update(over)
+    return lib.fd_paged_decode_partial(
+        a["q"], a["qss"], a["qsh"], a["k"], a["v"], a["sb"], a["sh"], a["st"], a["nblk"],
+        a["bt"], a["bts"], a["btw"], a["lens"], a["n"], a["H"], a["KVH"], a["D"], a["BS"],
+        a["scale"], a["dt"], a["out"], a["oss"], a["osh"], a["odt"], a["lse"], a["lsh"],
+        a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize(
+    "over,code",
+    [
+        (dict(H=6, KVH=4), _lib.FD_ERR_INVALID),          # H % KVH != 0
+        (dict(n=-1), _lib.FD_ERR_INVALID),
+        (dict(D=1024), _lib.FD_ERR_UNSUPPORTED),
+        (dict(dt=7), _lib.FD_ERR_INVALID),
+        (dict(odt=1), _lib.FD_ERR_INVALID),                # out bf16 with fp16 KV
+        (dict(q=None), _lib.FD_ERR_INVALID),
+        (dict(bts=2), _lib.FD_ERR_INVALID),                # row stride < width
+        (dict(scale=float("nan")), _lib.FD_ERR_INVALID),
+        (dict(BS=0), _lib.FD_ERR_INVALID),
+        # a wide table splits rows, and the split partials need workspace
+        (dict(ws=None, wsb=0, btw=256, bts=256), _lib.FD_ERR_WORKSPACE),
+    ],
+)
+def test_decode_rejects_bad_arguments_on_host(over, code):
+    lib = _lib.load_lib()
+    assert _decode(lib, **over) == code
+    assert lib.fd_last_error()
+
+
+def test_decode_n_zero_is_a_no_op():
+    assert _decode(_lib.load_lib(), n=0) == _lib.FD_OK
+
+
+def test_merge_and_cache_write_reject_bad_arguments():
+    lib = _lib.load_lib()
+    assert lib.fd_merge_attn_states(16, 64, 64, 9, 16, 64, 64, 0, 16, 1, 16, 64, 64, 0, 16, 1,
+                                    None, 0, 1, 1, 64, None) == _lib.FD_ERR_INVALID
+    assert lib.fd_merge_attn_states(None, 64, 64, 0, 16, 64, 64, 0, 16, 1, 16, 64, 64, 0, 16, 1,
+                                    None, 0, 1, 1, 64, None) == _lib.FD_ERR_INVALID
+    assert lib.fd_merge_attn_states(None, 64, 64, 0, None, 64, 64, 0, None, 1, None, 64, 64, 0,
+                                    None, 1, None, 0, 0, 1, 64, None) == _lib.FD_OK  # empty
+    assert lib.fd_reshape_and_cache(16, 64, 64, 16, 64, 64, 16, 16, 1, 1, 1, 4, None, 3, 1, 64,
+                                     16, 0, None, None) == _lib.FD_ERR_INVALID
+    assert lib.fd_reshape_and_cache(16, 64, 64, 16, 64, 64, 16, 16, 1, 1, 1, 4, 16, 3, 0, 64,
+                                    16, 0, None, None) == _lib.FD_ERR_INVALID
+    assert lib.fd_stream_copy(16, 16, 17, None) == _lib.FD_ERR_INVALID
+    assert lib.fd_host_device_pointer(None, None) == _lib.FD_ERR_INVALID

@@ -216,3 +216,31 @@ def test_full_size_workloads_match_oracle(gpu, name):
     assert st == 0
     assert_out_close(o, ref_out, 2e-3)
     assert_lse_close(l, ref_lse)
+
+
+@pytest.mark.skip(reason="covers the persistent work-queue decode kernel, which faulted the GPU "
+                         "on its first run with no cause found by reading; that code path was "
+                         "removed, so this test has nothing to run against")
+def test_counters_left_zero_across_calls(gpu, monkeypatch):
+    """The task queue and split-arrival counters are reset by every launch, so
+    calls of different shapes can share one counter array."""
+    from vllm_fastdecoder_amd.ops import WORKSPACE
+
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    k, v, _ = cases.kv_pool(w, pool, "host", gpu)
+    q = cases.queries(w, gpu)
+    ref = None
+    for split in ("1", "5", "16", "64", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        for n in (w.n, 3):
+            out = torch.empty(n, w.H, w.D, dtype=torch.float32, device=gpu)
+            lse = torch.empty(w.H, n, dtype=torch.float32, device=gpu)
+            ops.decode_attn(q[:n], k, v, bt[:n].to(gpu), lens[:n].to(gpu), w.scale, out, lse)
+            torch.cuda.synchronize()
+            for key, ctr in WORKSPACE._counters.items():
+                assert int(ctr.abs().sum()) == 0, (split, n)
+            if n == w.n:
+                if ref is None:
+                    ref = out.clone()
+                assert float((out - ref).abs().max()) < 1e-5
