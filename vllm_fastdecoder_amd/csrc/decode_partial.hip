@@ -8,11 +8,14 @@
 // out = 0 and lse = -inf for an empty row (cpu_attn.cpp:324-331).
 //
 // Work decomposition (memory-bound design):
-//   * one wavefront task = (sequence, kv head, range of `split_blocks`
-//     blocks); four independent tasks share a 256-thread workgroup so a CU
-//     can hold its full 32 waves;
-//   * a block of 16 tokens is read as 16-byte vector loads: a token row of
-//     D elements is spread over LPT = D/8 lanes, so one load instruction moves
+//   * a task = (sequence, kv head, range of up to `split_blocks` blocks) is
+//     one 256-thread workgroup; its 4 wavefronts take the range's blocks
+//     round-robin and each keeps its own softmax state, merged once through
+//     LDS at the end. At the vicuna-7b shape a task covers a whole sequence,
+//     so no second pass is needed; longer rows are split and a small combine
+//     kernel merges the split partials;
+//   * a block of 16 tokens is read as 16-byte buffer loads: a token row of D
+//     elements is spread over LPT = D/8 lanes, so one load instruction moves
 //     64/LPT whole rows (1 KiB for D = 128) and the wave's lanes form
 //     TPW = 64/LPT "rows" that each own a token of every load;
 //   * the next block's K and V are in flight (register double buffer) while
@@ -20,19 +23,19 @@
 //   * q.k: v_dot2_f32_{f16,bf16} on packed pairs, then a DPP butterfly over
 //     the LPT lanes of a token (fp32 throughout);
 //   * online softmax in the exp2 domain, kept independently per lane-row
-//     (no cross-row traffic in the main loop), rows and splits are merged once
-//     at the end with the same log-sum-exp rule as the tier merge;
+//     (no cross-row traffic in the main loop); rows, then waves, are merged at
+//     the end with the log-sum-exp rule of the tier merge;
 //   * the G = H/KVH query heads of a kv head share every K/V load.
-// Splits of one (sequence, head) are combined by a second small kernel.
 #include "fd_common.h"
 
 namespace fd {
 
 namespace {
 
-constexpr int kTileTokens = 16;   // tokens per block in the tiled kernel
-constexpr int kTasksPerGroup = 4; // independent wavefront tasks per workgroup
-constexpr int kMaxSplitBlocks = kWave;  // a split's block ids fit one VGPR
+constexpr int kTileTokens = 16;         // tokens per block in the tiled kernel
+constexpr int kWavesPerTask = 4;        // wavefronts sharing one task
+constexpr int kMaxWaveBlocks = kWave;   // a wave's block ids of a task fit one VGPR
+constexpr int kMaxSplitBlocks = kWavesPerTask * kMaxWaveBlocks;
 
 struct TiledParams {
   const uint16_t* q;
@@ -41,7 +44,7 @@ struct TiledParams {
   const uint16_t* v;
   int64_t kv_sb, kv_sh, kv_st;
   int64_t num_blocks;
-  uint32_t run_bytes;  // extent of one (block, head) run: 15 * kv_st + D elements
+  uint32_t run_bytes;  // extent of one (block, head) run: (15 * kv_st + D) elements
   const int32_t* bt;
   int64_t bt_stride;
   int32_t bt_width;
@@ -55,9 +58,8 @@ struct TiledParams {
   int64_t lse_sh;
   float* part_o;    // [n, H, S, D] fp32 (normalised partial outputs)
   float* part_lse;  // [n, H, S] fp32 (natural-log LSE of each partial)
-  int32_t S;        // max splits per (sequence, head)
+  int32_t S;        // max splits per (sequence, kv head)
   int32_t split_blocks;
-  int32_t tasks;    // n * KVH * S
 };
 
 // 16 bytes of 16-bit elements (8 values).
@@ -103,8 +105,7 @@ __device__ __forceinline__ void axpy8(float p, const Vec8& v, float* acc) {
 
 // Writes 8 consecutive outputs starting at element `off` of `out`.
 template <typename T>
-__device__ __forceinline__ void store8(void* out, int64_t off, bool f32,
-                                       const float* o) {
+__device__ __forceinline__ void store8(void* out, int64_t off, bool f32, const float* o) {
   if (f32) {
     float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + off);
     p[0] = make_float4(o[0], o[1], o[2], o[3]);
@@ -121,41 +122,46 @@ __device__ __forceinline__ void store8(void* out, int64_t off, bool f32,
 
 // Tiled kernel: block_size == 16, D in {64, 128, 256}, G in {1, 2, 4, 8},
 // 16-bit KV, every stride a multiple of 8 elements and 16-byte aligned bases.
+// One workgroup (4 waves) per task; grid = n * KVH * S tasks.
 template <typename T, int D, int G>
-__global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
-    TiledParams p) {
-  constexpr int LPT = D / 8;              // lanes per token row
-  constexpr int TPW = kWave / LPT;        // token rows per load instruction
+__global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(TiledParams p) {
+  constexpr int LPT = D / 8;                // lanes per token row
+  constexpr int TPW = kWave / LPT;          // token rows per load instruction
   constexpr int STEPS = kTileTokens / TPW;  // loads per block per lane
 
+  // per-wave softmax states for the cross-wave merge (log2-domain max, sum,
+  // unnormalised accumulator)
+  __shared__ float s_acc[kWavesPerTask][G][D];
+  __shared__ float s_m[kWavesPerTask][G];
+  __shared__ float s_l[kWavesPerTask][G];
+  __shared__ int s_bad[kWavesPerTask];
+
   const int lane = threadIdx.x & (kWave - 1);
-  // The wave index is uniform across the wave; readfirstlane puts it (and all
-  // task indexing derived from it) in scalar registers, so block-table and
-  // length reads become scalar loads and block bases scalar adds.
+  // The wave index is uniform across the wave; readfirstlane keeps it (and all
+  // indexing derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int task = blockIdx.x * kTasksPerGroup + wave;
-  if (task >= p.tasks) return;
+  const int task = blockIdx.x;
   // task -> (kv head fastest, then split, then sequence)
   const int kh = task % p.KVH;
   const int rest = task / p.KVH;
   const int split = rest % p.S;
   const int i = rest / p.S;
 
-  const int row = lane / LPT;  // which token of each load this lane owns
+  const int row = lane / LPT;    // which token of each load this lane owns
   const int chunk = lane % LPT;  // which 8-element slice of the row
 
   const int L = p.lens[i];
   const int nb = L > 0 ? (L + kTileTokens - 1) / kTileTokens : 0;
   const int b_begin = split * p.split_blocks;
-  if (split > 0 && b_begin >= nb) return;  // nothing left for this split
+  if (split > 0 && b_begin >= nb) return;  // nothing left for this split (whole group)
   const int b_end = min(nb, b_begin + p.split_blocks);
   const int nsplit = nb > 0 ? (nb + p.split_blocks - 1) / p.split_blocks : 1;
   const bool range_bad = L > p.bt_width * kTileTokens;
 
-  // ---- empty row or bad length: split 0 writes the final result directly
+  // ---- empty row or bad length: split 0, wave 0 writes the final result
   if (nb == 0 || range_bad) {
-    if (split > 0) return;
-    if (chunk == lane) {  // lanes 0 .. LPT-1 write
+    if (split > 0 || wave > 0) return;
+    if (lane < LPT) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const int h = kh * G + g;
@@ -163,9 +169,8 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
         const float fill = range_bad ? qnan() : 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = fill;
-        store8<T>(p.out, (int64_t)i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8,
-                  p.out_f32, o);
-        if (chunk == 0) p.lse[(int64_t)h * p.lse_sh + i] = range_bad ? qnan() : neg_inf();
+        store8<T>(p.out, (int64_t)i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8, p.out_f32, o);
+        if (lane == 0) p.lse[(int64_t)h * p.lse_sh + i] = range_bad ? qnan() : neg_inf();
       }
     }
     return;
@@ -198,18 +203,23 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
   }
 
-  // The split's block ids, one per lane (split_blocks <= 64), read once and
-  // range-checked together; the loop picks them with v_readlane.
-  const int nblk = b_end - b_begin;
-  int my_bid = lane < nblk ? p.bt[(int64_t)i * p.bt_stride + b_begin + lane] : 0;
-  const bool my_bad = lane < nblk && (my_bid < 0 || (int64_t)my_bid >= p.num_blocks);
+  // This wave's blocks are b_begin + wave + 4k. Their ids are read once, one
+  // per lane (at most 64), range-checked together and picked with v_readlane.
+  const int first = b_begin + wave;
+  const int nw = first < b_end ? (b_end - first + kWavesPerTask - 1) / kWavesPerTask : 0;
+  int my_bid = lane < nw ? p.bt[(int64_t)i * p.bt_stride + first + kWavesPerTask * lane] : 0;
+  const bool my_bad = lane < nw && (my_bid < 0 || (int64_t)my_bid >= p.num_blocks);
   const bool bad_block = __ballot(my_bad) != 0;
   my_bid = my_bad ? 0 : my_bid;  // keep every read inside the cache
 
-  // Element offset of the split's b-th block for this kv head; wave-uniform.
-  auto block_base = [&](int b) -> int64_t {
-    const int bid = __builtin_amdgcn_readlane(my_bid, b - b_begin);
+  // Element offset of this wave's k-th block for this kv head; wave-uniform.
+  auto block_base = [&](int k) -> int64_t {
+    const int bid = __builtin_amdgcn_readlane(my_bid, k);
     return (int64_t)bid * p.kv_sb + head_off;
+  };
+  // Valid tokens of this wave's k-th block (< 16 only for the row's last block).
+  auto block_tokens = [&](int k) -> int {
+    return min(kTileTokens, L - (first + kWavesPerTask * k) * kTileTokens);
   };
 
   Vec8 kb[2][STEPS], vb[2][STEPS];
@@ -271,25 +281,25 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
   // ---- main loop: two blocks per iteration, ping-ponging register buffers.
   // Loads inside the steady-state body are unconditional so the compiler's
   // wait counts only cover the block being reduced, never its successor.
-  int b = b_begin;
-  load_block(0, block_base(b));
-  for (; b + 2 < b_end; b += 2) {
-    load_block(1, block_base(b + 1));
-    compute_block(0, kTileTokens);  // never the last block of the sequence
-    load_block(0, block_base(b + 2));
-    compute_block(1, kTileTokens);
-  }
-  if (b + 1 < b_end) {
-    load_block(1, block_base(b + 1));
-    compute_block(0, kTileTokens);
-    compute_block(1, min(kTileTokens, L - (b + 1) * kTileTokens));
-  } else {
-    compute_block(0, min(kTileTokens, L - b * kTileTokens));
+  if (nw > 0) {
+    int k = 0;
+    load_block(0, block_base(0));
+    for (; k + 2 < nw; k += 2) {
+      load_block(1, block_base(k + 1));
+      compute_block(0, block_tokens(k));
+      load_block(0, block_base(k + 2));
+      compute_block(1, block_tokens(k + 1));
+    }
+    if (k + 1 < nw) {
+      load_block(1, block_base(k + 1));
+      compute_block(0, block_tokens(k));
+      compute_block(1, block_tokens(k + 1));
+    } else {
+      compute_block(0, block_tokens(k));
+    }
   }
 
-  // ---- merge the TPW lane-rows of each head, then write
-  constexpr int kRowsMask = kWave - LPT;  // xor masks that cross rows
-  const bool write_final = nsplit == 1;
+  // ---- merge the TPW lane-rows of each head into this wave's state, publish it
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float M = m[g];
@@ -307,12 +317,59 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] += shfl_xor_f32(o[e], x);
     }
-    (void)kRowsMask;
+    if (lane < LPT) {
+      float4* dst = reinterpret_cast<float4*>(&s_acc[wave][g][chunk * 8]);
+      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (lane == 0) {
+      s_m[wave][g] = M;
+      s_l[wave][g] = lt;
+    }
+  }
+  if (lane == 0) s_bad[wave] = bad_block ? 1 : 0;
+  __syncthreads();
+  if (wave != 0) return;
+
+  // ---- wave 0: merge the waves' states and write the final result or this
+  // split's partial
+  bool bad = false;
+#pragma unroll
+  for (int w = 0; w < kWavesPerTask; ++w) bad |= s_bad[w] != 0;
+  const bool write_final = nsplit == 1;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = s_m[0][g];
+#pragma unroll
+    for (int w = 1; w < kWavesPerTask; ++w) M = fmaxf(M, s_m[w][g]);
+    const float Ms = M == neg_inf() ? 0.f : M;
+    float lt = 0.f;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerTask; ++w) {
+      const float sc = fast_exp2(s_m[w][g] - Ms);  // 0 for a wave without blocks
+      lt += sc * s_l[w][g];
+      if (lane < LPT) {
+        const float4* src = reinterpret_cast<const float4*>(&s_acc[w][g][chunk * 8]);
+        const float4 a = src[0];
+        const float4 b = src[1];
+        o[0] += sc * a.x;
+        o[1] += sc * a.y;
+        o[2] += sc * a.z;
+        o[3] += sc * a.w;
+        o[4] += sc * b.x;
+        o[5] += sc * b.y;
+        o[6] += sc * b.z;
+        o[7] += sc * b.w;
+      }
+    }
     const float inv = 1.f / lt;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] *= inv;
     float lse_nat = (M + fast_log2(lt)) * kLn2;
-    if (bad_block) {
+    if (bad) {
       lse_nat = qnan();
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = qnan();
@@ -320,8 +377,7 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
     const int h = kh * G + g;
     if (lane < LPT) {
       if (write_final) {
-        store8<T>(p.out, (int64_t)i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8,
-                  p.out_f32, o);
+        store8<T>(p.out, (int64_t)i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8, p.out_f32, o);
         if (lane == 0) p.lse[(int64_t)h * p.lse_sh + i] = lse_nat;
       } else {
         const int64_t pidx = ((int64_t)i * p.H + h) * p.S + split;
@@ -333,15 +389,19 @@ __global__ __launch_bounds__(kWave * kTasksPerGroup) void decode_tiled_kernel(
 }
 
 // Combines the split partials of every (sequence, head) whose sequence used
-// more than one split: the N-way form of the log-sum-exp merge.
+// more than one split: the N-way form of the log-sum-exp merge. One thread
+// per 4 output elements; each thread reads the row's split LSEs (L1-shared
+// with its neighbours) and its slice of every split's partial.
 __global__ __launch_bounds__(256) void combine_splits_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ lens, int32_t n, int32_t H, int32_t D, int32_t S,
     int32_t split_blocks, int32_t block_size, int32_t bt_width, void* out, int64_t out_ss,
     int64_t out_sh, int32_t out_dt, float* lse, int64_t lse_sh) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pair >= (int64_t)n * H) return;
+  const int per_row = D / 4;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (tid >= (int64_t)n * H * per_row) return;
+  const int c = (int)(tid % per_row);
+  const int64_t pair = tid / per_row;
   const int i = (int)(pair / H);
   const int h = (int)(pair % H);
   const int L = lens[i];
@@ -354,15 +414,25 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(
   for (int s = 0; s < ns; ++s) M = fmaxf(M, pl[s]);
   const float Ms = M == neg_inf() ? 0.f : M;
   float wsum = 0.f;
-  for (int s = 0; s < ns; ++s) wsum += __expf(pl[s] - Ms);
-  const float inv = 1.f / wsum;
-  const float* po = part_o + pair * S * D;
-  for (int d = lane; d < D; d += kWave) {
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) acc += __expf(pl[s] - Ms) * po[(int64_t)s * D + d];
-    store_elem(out, (int64_t)i * out_ss + (int64_t)h * out_sh + d, out_dt, acc * inv);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const float4* po = reinterpret_cast<const float4*>(part_o + pair * S * D) + c;
+#pragma unroll 4
+  for (int s = 0; s < ns; ++s) {
+    const float w = __expf(pl[s] - Ms);
+    const float4 x = po[(int64_t)s * (D / 4)];
+    wsum += w;
+    acc.x += w * x.x;
+    acc.y += w * x.y;
+    acc.z += w * x.z;
+    acc.w += w * x.w;
   }
-  if (lane == 0) lse[(int64_t)h * lse_sh + i] = Ms + __logf(wsum);
+  const float inv = 1.f / wsum;
+  const int64_t ob = (int64_t)i * out_ss + (int64_t)h * out_sh + c * 4;
+  store_elem(out, ob + 0, out_dt, acc.x * inv);
+  store_elem(out, ob + 1, out_dt, acc.y * inv);
+  store_elem(out, ob + 2, out_dt, acc.z * inv);
+  store_elem(out, ob + 3, out_dt, acc.w * inv);
+  if (c == 0) lse[(int64_t)h * lse_sh + i] = Ms + __logf(wsum);
 }
 
 // Generic kernel: any head_size, block_size, group size and dtype (including
@@ -431,37 +501,36 @@ __global__ __launch_bounds__(kWave) void decode_generic_kernel(
   if (lane == 0) lse[(int64_t)h * lse_sh + i] = bad ? qnan() : mrun + __logf(lrun);
 }
 
-// FD_SPLIT_BLOCKS=<n> forces n blocks per split task (tuning and tests).
+// FD_SPLIT_BLOCKS=<n> forces n blocks per task (tuning and tests).
 int split_blocks_override() {
   const char* e = getenv("FD_SPLIT_BLOCKS");
   return e ? atoi(e) : 0;
 }
 
 template <typename T, int D, int G>
-hipError_t launch_tiled(const TiledParams& tp, hipStream_t s) {
-  const int groups = (tp.tasks + kTasksPerGroup - 1) / kTasksPerGroup;
-  hipLaunchKernelGGL((decode_tiled_kernel<T, D, G>), dim3(groups),
-                     dim3(kWave * kTasksPerGroup), 0, s, tp);
+hipError_t launch_tiled(const TiledParams& tp, unsigned tasks, hipStream_t s) {
+  hipLaunchKernelGGL((decode_tiled_kernel<T, D, G>), dim3(tasks), dim3(kWave * kWavesPerTask),
+                     0, s, tp);
   return hipGetLastError();
 }
 
 template <typename T, int D>
-hipError_t dispatch_g(const TiledParams& tp, int G, hipStream_t s) {
+hipError_t dispatch_g(const TiledParams& tp, unsigned tasks, int G, hipStream_t s) {
   switch (G) {
-    case 1: return launch_tiled<T, D, 1>(tp, s);
-    case 2: return launch_tiled<T, D, 2>(tp, s);
-    case 4: return launch_tiled<T, D, 4>(tp, s);
-    case 8: return launch_tiled<T, D, 8>(tp, s);
+    case 1: return launch_tiled<T, D, 1>(tp, tasks, s);
+    case 2: return launch_tiled<T, D, 2>(tp, tasks, s);
+    case 4: return launch_tiled<T, D, 4>(tp, tasks, s);
+    case 8: return launch_tiled<T, D, 8>(tp, tasks, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <typename T>
-hipError_t dispatch_d(const TiledParams& tp, int D, int G, hipStream_t s) {
+hipError_t dispatch_d(const TiledParams& tp, unsigned tasks, int D, int G, hipStream_t s) {
   switch (D) {
-    case 64: return dispatch_g<T, 64>(tp, G, s);
-    case 128: return dispatch_g<T, 128>(tp, G, s);
-    case 256: return dispatch_g<T, 256>(tp, G, s);
+    case 64: return dispatch_g<T, 64>(tp, tasks, G, s);
+    case 128: return dispatch_g<T, 128>(tp, tasks, G, s);
+    case 256: return dispatch_g<T, 256>(tp, tasks, G, s);
   }
   return hipErrorInvalidValue;
 }
@@ -481,14 +550,14 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     return sp;
   }
   int sb = split_blocks_override();
-  if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // one block id per lane
+  if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   if (sb <= 0) {
-    // Enough wavefront tasks to cover every CU several times over, without
-    // cutting a sequence into tiny pieces: 8 blocks (128 tokens) per task
-    // unless the batch already supplies the parallelism.
+    // Whole rows per workgroup (32 blocks per wave) while the batch alone
+    // supplies >= 2048 workgroups (8 per CU); shorter tasks otherwise, down
+    // to 4 blocks per wave.
     const int64_t pairs = (int64_t)n * KVH;
-    sb = 8;
-    while (sb < kMaxSplitBlocks && pairs * ((bt_width + 2 * sb - 1) / (2 * sb)) >= 32768) sb *= 2;
+    sb = 128;
+    while (sb > 16 && pairs * ((bt_width + sb - 1) / sb) < 2048) sb /= 2;
   }
   sp.split_blocks = sb;
   sp.max_splits = bt_width > 0 ? (bt_width + sb - 1) / sb : 1;
@@ -546,16 +615,15 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     tp.part_lse = reinterpret_cast<float*>(ws + parts * a.D * sizeof(float));
   }
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.max_splits;
-  if (tasks > INT32_MAX / 2) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
-  tp.tasks = (int32_t)tasks;
+  if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
   const int G = a.H / a.KVH;
-  hipError_t e = a.kv_dtype == FD_F16 ? dispatch_d<F16>(tp, a.D, G, s)
-                                      : dispatch_d<BF16>(tp, a.D, G, s);
+  hipError_t e = a.kv_dtype == FD_F16 ? dispatch_d<F16>(tp, (unsigned)tasks, a.D, G, s)
+                                      : dispatch_d<BF16>(tp, (unsigned)tasks, a.D, G, s);
   if (e != hipSuccess) return hip_error(e, "decode_tiled_kernel launch");
   if (sp.max_splits > 1) {
-    const int64_t pairs = (int64_t)a.n * a.H;
-    hipLaunchKernelGGL(combine_splits_kernel, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0,
-                       s, tp.part_o, tp.part_lse, a.lens, a.n, a.H, a.D, sp.max_splits,
+    const int64_t threads = (int64_t)a.n * a.H * (a.D / 4);
+    hipLaunchKernelGGL(combine_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
+                       0, s, tp.part_o, tp.part_lse, a.lens, a.n, a.H, a.D, sp.max_splits,
                        sp.split_blocks, kTileTokens, a.bt_width, a.out, a.out_ss, a.out_sh,
                        a.out_dtype, a.lse, a.lse_sh);
     e = hipGetLastError();
