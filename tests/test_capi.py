@@ -49,9 +49,13 @@ def test_check_slots_host_rule():
 def test_workspace_size_query():
     lib = _lib.load_lib()
     size = ctypes.c_size_t()
-    # vicuna-7b shape: 128 sequences, 32/32 heads, width 128 blocks
+    # vicuna-7b shape (128 sequences, 32/32 heads, width 128 blocks): one
+    # workgroup covers a whole row, no split partials
     assert lib.fd_paged_decode_workspace_size(128, 32, 32, 128, 16, 128, ctypes.byref(size)) == 0
-    assert size.value > 0
+    assert size.value == 0
+    # 16k-token rows are split: partials need workspace
+    assert lib.fd_paged_decode_workspace_size(128, 32, 32, 128, 16, 1024, ctypes.byref(size)) == 0
+    assert size.value >= 128 * 32 * 8 * 128 * 4
     # a head size the tiled kernel does not take needs no workspace
     assert lib.fd_paged_decode_workspace_size(7, 8, 8, 72, 16, 6, ctypes.byref(size)) == 0
     assert size.value == 0
