@@ -1,0 +1,176 @@
+"""Split decode path on MI355X: the GPU-op seam and the per-layer orchestration.
+
+Mirrors the reference backend's hot path (fastdecode/backend.py) without
+vLLM's base classes:
+
+  * `HipOps` / `OPS` -- the seam of backend.py:42-64 (`fa`, `reshape_and_cache`,
+    `merge`, `event`), routed to libfdattn. `fa` implements the paged decode
+    form the split path uses (one query token per row, block table,
+    return_softmax_lse); prefill forms raise NotImplementedError (FlashAttention
+    prefill is not on this path). Tests swap OPS the way the reference's tests
+    do (tests/test_plan_and_forward.py:106-113).
+  * `build_split_plan` -- FastDecodeMetadataBuilder.build (backend.py:140-178):
+    one device-to-host copy of the step's block table and slots, the host
+    planner, then the device plan.
+  * `SplitDecodeImpl._forward_split` -- FastDecodeImpl._forward_split
+    (backend.py:257-357). The structure is the reference's; the host tier is
+    no longer computed on the host: its KV rows are written into the pinned
+    tier by the GPU and its partial is read zero-copy by the GPU, so there is
+    no staging copy and no host wait.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import ops, state
+from .plan import DevicePlan, build_host_plan, to_device
+
+
+class HipOps:
+    """GPU primitives of the split path (swapped for stand-ins in tests)."""
+
+    @staticmethod
+    def fa(q, k, v, cu_seqlens_q=None, max_seqlen_q=1, seqused_k=None, max_seqlen_k=None,
+           softmax_scale=None, causal=False, block_table=None, softcap=0.0,
+           return_softmax_lse=False, out=None, **_):
+        """Paged decode partial in flash_attn_varlen_func's calling convention
+        (backend.py:306-314): k/v are the [B, BS, KVH, D] cache views, one query
+        token per row, seqused_k the per-row token counts (0 allowed)."""
+        if block_table is None or max_seqlen_q != 1 or seqused_k is None:
+            raise NotImplementedError("HipOps.fa: only the paged decode form (one query "
+                                      "token per row with a block table) is implemented")
+        if softcap:
+            raise NotImplementedError("HipOps.fa: logits soft-cap is not supported")
+        o, lse = ops.paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=out)
+        return (o, lse) if return_softmax_lse else o
+
+    @staticmethod
+    def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype="auto",
+                          k_scale=None, v_scale=None):
+        ops.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype)
+
+    @staticmethod
+    def merge(out, o_a, lse_a, o_b, lse_b):
+        ops.merge_attn_states(out, o_a, lse_a, o_b, lse_b)
+
+    @staticmethod
+    def event():
+        ev = torch.cuda.Event()
+        ev.record()
+        return ev
+
+
+OPS = HipOps
+
+
+def build_split_plan(query_start_loc_cpu: torch.Tensor, seq_lens_cpu: torch.Tensor,
+                     block_table: torch.Tensor, slot_mapping: torch.Tensor, num_reqs: int,
+                     store: state.HostKVStore | None, device) -> DevicePlan | None:
+    """Per-step plan (backend.py:140-178): None when no host tier is set up or
+    no request touches it (the step then runs plain paged attention)."""
+    if store is None or num_reqs == 0:
+        return None
+    bs = store.block_size
+    qsl = query_start_loc_cpu[: num_reqs + 1]
+    seq = seq_lens_cpu[:num_reqs]
+    max_blocks = int((int(seq.max()) + bs - 1) // bs)
+    width = max(1, min(max_blocks, block_table.shape[1]))
+    bt_dev = block_table[:num_reqs]
+    n_tok = int(qsl[-1])
+    bt = bt_dev[:, :width].cpu()  # the step's one device-to-host sync
+    slots = slot_mapping[:n_tok].cpu()
+    hp = build_host_plan(qsl, seq, bt, slots, store.num_gpu_blocks, store.num_cpu_blocks, bs)
+    if hp is None:
+        return None
+    return to_device(hp, bt_dev[:, :width], device)
+
+
+@dataclass
+class SplitDecodeImpl:
+    """The attention-layer state the split path needs (FastDecodeImpl's
+    fields, backend.py:200-214)."""
+
+    num_heads: int
+    num_kv_heads: int
+    head_size: int
+    scale: float
+    kv_cache_dtype: str = "auto"
+    logits_soft_cap: float = 0.0
+    kv_sharing_target_layer_name: str | None = None
+
+    def _forward_split(self, layer, query, key, value, kv_cache, dp: DevicePlan, output):
+        """query [T, H, D]; key/value [T, KVH, D] (possibly strided views);
+        kv_cache the logical [B, KVH, BS, 2D] view of the HBM tier; output
+        [T, H, D], written for the plan's S, P and F token rows."""
+        hp = dp.host
+        store = state.STORE
+        assert store is not None, "no host KV tier (state.ensure_store)"
+        k_host = store.k[layer.layer_name]
+        v_host = store.v[layer.layer_name]
+        fa = OPS.fa
+        H, D = self.num_heads, self.head_size
+        key_cache, value_cache = kv_cache.transpose(1, 2).split(D, dim=-1)
+
+        # 1) KV writes: HBM slots by reshape_and_cache (host slots are -1), host
+        #    slots straight into the pinned tier by the GPU (no staging copy)
+        if self.kv_sharing_target_layer_name is None:
+            OPS.reshape_and_cache(key, value, key_cache, value_cache, dp.gpu_slot_mapping,
+                                  self.kv_cache_dtype, getattr(layer, "_k_scale", None),
+                                  getattr(layer, "_v_scale", None))
+            if hp.cpu_w_tok.numel():
+                kw = key.index_select(0, dp.cpu_w_tok)
+                vw = value.index_select(0, dp.cpu_w_tok)
+                ops.store_kv(kw, vw, hp.cpu_w_slot, k_host, v_host)
+
+        # 2) split decodes: HBM-tier and host-tier partials, both on the GPU.
+        #    Rows without HBM tokens come back as (0, -inf) from the kernel, so
+        #    every S row goes in as is.
+        ns = hp.n_s
+        if ns:
+            qs = query.index_select(0, dp.s_tok)
+            if hp.s_max_gpu_len > 0:
+                o_gpu, lse_gpu = fa(
+                    q=qs, k=key_cache, v=value_cache,
+                    cu_seqlens_q=torch.arange(ns + 1, dtype=torch.int32, device=qs.device),
+                    max_seqlen_q=1, seqused_k=dp.s_gpu_lens_all, max_seqlen_k=hp.s_max_gpu_len,
+                    softmax_scale=self.scale, causal=False, block_table=dp.s_gpu_bt_all,
+                    softcap=self.logits_soft_cap, return_softmax_lse=True, num_splits=1,
+                )
+            else:
+                o_gpu = torch.zeros_like(qs)
+                lse_gpu = torch.full((H, ns), float("-inf"), dtype=torch.float32, device=qs.device)
+            o_cpu = torch.empty_like(qs)
+            lse_cpu = torch.empty(H, ns, dtype=torch.float32, device=qs.device)
+            ops.decode_attn(qs, k_host, v_host, dp.s_cpu_bt, dp.s_cpu_lens, float(self.scale),
+                            o_cpu, lse_cpu)
+
+        # 3) attention that touches no host block: P (all-HBM requests) and F
+        #    (fresh prefills over this step's q/k/v) -- prefill forms of OPS.fa
+        if hp.n_p_tok:
+            q_p = query.index_select(0, dp.p_tok)
+            o_p = fa(
+                q=q_p, k=key_cache, v=value_cache, cu_seqlens_q=dp.p_cu, max_seqlen_q=hp.p_max_q,
+                seqused_k=dp.p_seqlens, max_seqlen_k=hp.p_max_k, softmax_scale=self.scale,
+                causal=True, block_table=dp.p_bt, softcap=self.logits_soft_cap,
+            )
+            output.index_copy_(0, dp.p_tok, o_p)
+        if hp.n_f_tok:
+            q_f = query.index_select(0, dp.f_tok)
+            k_f = key.index_select(0, dp.f_tok)
+            v_f = value.index_select(0, dp.f_tok)
+            o_f = fa(
+                q=q_f, k=k_f, v=v_f, cu_seqlens_q=dp.f_cu, cu_seqlens_k=dp.f_cu,
+                max_seqlen_q=hp.f_max, max_seqlen_k=hp.f_max, softmax_scale=self.scale,
+                causal=True, softcap=self.logits_soft_cap,
+            )
+            output.index_copy_(0, dp.f_tok, o_f)
+
+        # 4) merge the split decodes' partials into their output rows
+        if ns:
+            merged = torch.empty_like(qs)
+            OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
+            output.index_copy_(0, dp.s_tok, merged)
+        return output

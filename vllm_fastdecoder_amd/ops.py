@@ -274,9 +274,12 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
              and key_cache.stride() == value_cache.stride(), "caches must be [B, BS, KVH, D]")
     B, BS, KVH, D = key_cache.shape
     _require(key.shape[1] == KVH and key.shape[2] == D, "key shape does not match the cache")
-    _cache_write(key, value, key_cache, value_cache,
+    # the token count is the slot mapping's; key/value may carry padding rows
+    T = slot_mapping.shape[0]
+    _require(key.shape[0] >= T and value.shape[0] >= T, "fewer key/value rows than slots")
+    _cache_write(key[:T], value[:T], key_cache, value_cache,
                  (key_cache.stride(0), key_cache.stride(1), key_cache.stride(2)),
-                 B, BS, slot_mapping[: key.shape[0]], error_count)
+                 B, BS, slot_mapping, error_count)
 
 
 def store_kv(k, v, slots, k_cache, v_cache) -> None:

@@ -1,0 +1,261 @@
+"""Per-step execution plan of the split decode path (host side).
+
+Block ids `< G` live in the HBM tier, ids `>= G` in the pinned host tier at
+`id - G` (fastdecode/plan.py:3-4). Every active request falls in one class
+(plan.py:6-10):
+
+  P  all of its blocks in HBM                 -> ordinary paged attention
+  S  a decode (one query token) touching the  -> HBM-tier partial + host-tier
+     host tier                                   partial, LSE-merged
+  F  a fresh prefill (no prior context)        -> attention over this step's
+     touching the host tier                      q/k/v only
+
+A request with prior context, more than one query token and host blocks (a
+chunked-prefill continuation or prefix hit) is rejected (plan.py:142-149).
+
+`build_host_plan` returns the same `HostPlan` fields, dtypes and values as
+the reference's planner (fastdecode/plan.py:26-199): stable per-tier block
+compaction, HBM tables zero-padded to a multiple of 16 columns, tier token
+counts from the tokens held by each block, host slots masked to -1 in the
+HBM slot mapping and rebased by `G * block_size` for the host tier. Beyond
+the reference it also returns `host_slot_mapping`: the whole step's slot
+mapping rebased to the host tier with HBM slots masked to -1, so one
+cache-write kernel can write the host tier in place (no gather, no staging).
+
+`to_device` mirrors fastdecode/plan.py:202-245.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+GPU_TABLE_PAD = 16  # HBM-tier tables are padded to a multiple of 16 columns (plan.py:171,195-201)
+
+
+@dataclass
+class HostPlan:
+    n_tok: int
+    # KV writes
+    gpu_slot_mapping: torch.Tensor  # [n_tok] int64, host-tier slots replaced by -1
+    cpu_w_tok: torch.Tensor  # [nw] int64 token rows whose KV goes to the host tier
+    cpu_w_slot: torch.Tensor  # [nw] int64 host-tier-relative slot ids
+    # P
+    p_tok: torch.Tensor  # [nP_tok] int64
+    p_cu: torch.Tensor  # [nP + 1] int32
+    p_seqlens: torch.Tensor  # [nP] int32
+    p_req: torch.Tensor  # [nP] int64 rows of the block table
+    p_max_q: int
+    p_max_k: int
+    # S
+    s_tok: torch.Tensor  # [nS] int64
+    s_gpu_bt: torch.Tensor  # [nS, Wg] int32 (HBM-tier block ids, compacted)
+    s_gpu_lens: torch.Tensor  # [nS] int32
+    s_max_gpu_len: int
+    s_cpu_bt: torch.Tensor  # [nS, Wc] int32 (host-tier-relative ids, compacted)
+    s_cpu_lens: torch.Tensor  # [nS] int32
+    # F
+    f_tok: torch.Tensor  # [nF_tok] int64
+    f_cu: torch.Tensor  # [nF + 1] int32
+    f_max: int
+    # this build: the step's slots rebased to the host tier, HBM slots -> -1
+    host_slot_mapping: torch.Tensor | None = None  # [n_tok] int64
+
+    @property
+    def n_s(self) -> int:
+        return int(self.s_tok.numel())
+
+    @property
+    def n_p_tok(self) -> int:
+        return int(self.p_tok.numel())
+
+    @property
+    def n_f_tok(self) -> int:
+        return int(self.f_tok.numel())
+
+
+def _token_runs(starts: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+    """The token indices start .. start + count - 1 of every run, in order."""
+    counts = counts.to(torch.int64)
+    total = int(counts.sum()) if counts.numel() else 0
+    if total == 0:
+        return torch.zeros(0, dtype=torch.int64)
+    run = torch.repeat_interleave(torch.arange(counts.numel()), counts)
+    first = torch.cumsum(counts, 0) - counts  # position of each run's first token
+    return starts.to(torch.int64)[run] + (torch.arange(total) - first[run])
+
+
+def _offsets(counts: torch.Tensor) -> torch.Tensor:
+    """[0, c0, c0 + c1, ...] as int32."""
+    out = torch.zeros(counts.numel() + 1, dtype=torch.int32)
+    if counts.numel():
+        out[1:] = torch.cumsum(counts.to(torch.int64), 0).to(torch.int32)
+    return out
+
+
+def compact_rows(table: torch.Tensor, keep: torch.Tensor, subtract: int, pad_to: int = 1) -> torch.Tensor:
+    """Per row, the kept entries moved to the front in their original order,
+    minus `subtract`; every other entry 0. Width: the largest kept count
+    (at least 1) rounded up to `pad_to` (fastdecode/plan.py:82-100)."""
+    rows, width_in = table.shape
+    if table.numel() == 0:
+        return torch.zeros(rows, pad_to, dtype=torch.int32)
+    per_row = keep.sum(1)
+    width = max(1, int(per_row.max()))
+    width = -(-width // pad_to) * pad_to
+    out = torch.zeros(rows, max(width, width_in), dtype=torch.int64)
+    r, c = keep.nonzero(as_tuple=True)  # row-major: stable inside each row
+    dest = (torch.cumsum(keep.to(torch.int64), 1) - 1)[r, c]
+    out[r, dest] = table[r, c].to(torch.int64) - subtract
+    return out[:, :width].to(torch.int32).contiguous()
+
+
+def build_host_plan(
+    query_start_loc: torch.Tensor,  # [R + 1] (cpu)
+    seq_lens: torch.Tensor,  # [R] (cpu), context + this step's tokens
+    block_table: torch.Tensor,  # [R, W] int32 (cpu), W >= ceil(max seq / bs)
+    slot_mapping: torch.Tensor,  # [>= n_tok] int64 (cpu)
+    num_gpu_blocks: int,
+    num_cpu_blocks: int,
+    block_size: int,
+) -> HostPlan | None:
+    G, bs = int(num_gpu_blocks), int(block_size)
+    qsl = query_start_loc.to(torch.int64)
+    lens = seq_lens.to(torch.int64)
+    qlen = qsl[1:] - qsl[:-1]
+    prior = lens - qlen
+    n_tok = int(qsl[-1]) if qsl.numel() else 0
+    slots = slot_mapping[:n_tok].to(torch.int64)
+
+    R, W = block_table.shape
+    col = torch.arange(W, dtype=torch.int64)
+    # tokens held by column c of each row: bs for full blocks, the remainder
+    # for the last one, 0 past the row's blocks
+    held = (lens[:, None] - col[None, :] * bs).clamp(min=0, max=bs)
+    used = held > 0
+    ids = block_table.to(torch.int64)
+    in_host = used & (ids >= G)
+    in_hbm = used & (ids < G)
+    touches_host = in_host.any(1)
+    host_slot = slots >= G * bs
+
+    if not bool(touches_host.any()) and not bool(host_slot.any()):
+        return None  # everything in HBM this step: plain paged attention
+
+    if bool(in_host.any()) and int(ids[in_host].max()) >= G + int(num_cpu_blocks):
+        raise RuntimeError(
+            "FastDecode: block id beyond GPU+CPU capacity; engine and worker "
+            "disagree on FASTDECODE_CPU_BLOCKS / FASTDECODE_CPU_KV_GB"
+        )
+
+    active = qlen > 0
+    is_s = active & touches_host & (qlen == 1)
+    is_f = active & touches_host & (qlen > 1) & (prior == 0)
+    if bool((active & touches_host & (qlen > 1) & (prior > 0)).any()):
+        raise NotImplementedError(
+            "FastDecode: a request with prior context is being extended by >1 token "
+            "while part of its KV is on the CPU (chunked prefill or prefix-cache hit). "
+            "Run with enable_prefix_caching=False and "
+            "max_num_batched_tokens >= max_model_len."
+        )
+    is_p = active & ~touches_host
+
+    minus_one = torch.full_like(slots, -1)
+    gpu_slot_mapping = torch.where(host_slot, minus_one, slots)
+    host_slot_mapping = torch.where(host_slot, slots - G * bs, minus_one)
+    cpu_w_tok = host_slot.nonzero().flatten()
+    cpu_w_slot = (slots[cpu_w_tok] - G * bs).contiguous()
+
+    p_req = is_p.nonzero().flatten()
+    p_q = qlen[p_req]
+    p_seqlens = lens[p_req].to(torch.int32)
+
+    s_req = is_s.nonzero().flatten()
+    s_held = held[s_req]
+    s_gpu_lens = (s_held * in_hbm[s_req]).sum(1).to(torch.int32)
+    s_cpu_lens = (s_held * in_host[s_req]).sum(1).to(torch.int32).contiguous()
+
+    f_req = is_f.nonzero().flatten()
+    f_q = qlen[f_req]
+
+    return HostPlan(
+        n_tok=n_tok,
+        gpu_slot_mapping=gpu_slot_mapping,
+        cpu_w_tok=cpu_w_tok,
+        cpu_w_slot=cpu_w_slot,
+        p_tok=_token_runs(qsl[p_req], p_q),
+        p_cu=_offsets(p_q),
+        p_seqlens=p_seqlens,
+        p_req=p_req,
+        p_max_q=int(p_q.max()) if p_q.numel() else 0,
+        p_max_k=int(p_seqlens.max()) if p_seqlens.numel() else 0,
+        s_tok=qsl[s_req],
+        s_gpu_bt=compact_rows(ids[s_req], in_hbm[s_req], 0, pad_to=GPU_TABLE_PAD),
+        s_gpu_lens=s_gpu_lens,
+        s_max_gpu_len=int(s_gpu_lens.max()) if s_gpu_lens.numel() else 0,
+        s_cpu_bt=compact_rows(ids[s_req], in_host[s_req], G),
+        s_cpu_lens=s_cpu_lens,
+        f_tok=_token_runs(qsl[f_req], f_q),
+        f_cu=_offsets(f_q),
+        f_max=int(f_q.max()) if f_q.numel() else 0,
+        host_slot_mapping=host_slot_mapping,
+    )
+
+
+@dataclass
+class DevicePlan:
+    """HostPlan with the tensors the GPU needs moved to the device
+    (fastdecode/plan.py:202-221)."""
+
+    host: HostPlan
+    gpu_slot_mapping: torch.Tensor
+    cpu_w_tok: torch.Tensor
+    p_tok: torch.Tensor
+    p_cu: torch.Tensor
+    p_seqlens: torch.Tensor
+    p_bt: torch.Tensor  # [nP, W] int32 rows of the batch block table
+    s_tok: torch.Tensor
+    # the S rows that hold HBM tokens (the reference hands only these to
+    # FlashAttention; this build's kernel also accepts empty rows)
+    s_gpu_rows: torch.Tensor  # [nG] int64, indices into the S rows
+    s_gpu_cu: torch.Tensor  # arange(nG + 1) int32
+    s_gpu_bt: torch.Tensor  # [nG, Wg] int32
+    s_gpu_lens: torch.Tensor  # [nG] int32, all > 0
+    f_tok: torch.Tensor
+    f_cu: torch.Tensor
+    # this build: every S row's tables on the device, and the host-tier writes
+    s_gpu_bt_all: torch.Tensor | None = None  # [nS, Wg] int32
+    s_gpu_lens_all: torch.Tensor | None = None  # [nS] int32
+    s_cpu_bt: torch.Tensor | None = None  # [nS, Wc] int32
+    s_cpu_lens: torch.Tensor | None = None  # [nS] int32
+    host_slot_mapping: torch.Tensor | None = None  # [n_tok] int64
+
+
+def to_device(hp: HostPlan, block_table_dev: torch.Tensor, device) -> DevicePlan:
+    def d(t: torch.Tensor) -> torch.Tensor:
+        return t.to(device, non_blocking=False)
+
+    g_rows = (hp.s_gpu_lens > 0).nonzero().flatten()
+    return DevicePlan(
+        host=hp,
+        gpu_slot_mapping=d(hp.gpu_slot_mapping),
+        cpu_w_tok=d(hp.cpu_w_tok),
+        p_tok=d(hp.p_tok),
+        p_cu=d(hp.p_cu),
+        p_seqlens=d(hp.p_seqlens),
+        p_bt=(block_table_dev.index_select(0, d(hp.p_req)) if hp.p_req.numel()
+              else block_table_dev[:0]),
+        s_tok=d(hp.s_tok),
+        s_gpu_rows=d(g_rows),
+        s_gpu_cu=torch.arange(g_rows.numel() + 1, dtype=torch.int32, device=device),
+        s_gpu_bt=d(hp.s_gpu_bt[g_rows]),
+        s_gpu_lens=d(hp.s_gpu_lens[g_rows]),
+        f_tok=d(hp.f_tok),
+        f_cu=d(hp.f_cu),
+        s_gpu_bt_all=d(hp.s_gpu_bt),
+        s_gpu_lens_all=d(hp.s_gpu_lens),
+        s_cpu_bt=d(hp.s_cpu_bt),
+        s_cpu_lens=d(hp.s_cpu_lens),
+        host_slot_mapping=d(hp.host_slot_mapping) if hp.host_slot_mapping is not None else None,
+    )
