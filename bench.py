@@ -200,6 +200,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
             t[s:e].copy_(torch.randn(e - s, w.KVH, w.BS, w.D, generator=gen, device=dev).to(w.dtype).cpu())
     bt_g_d, bt_c_d = bt_g.to(dev), bt_c.to(dev)
     len_g_d, len_c_d = len_g.to(dev), len_c.to(dev)
+    ord_g, ord_c = ops.longest_first(len_g).to(dev), ops.longest_first(len_c).to(dev)
     o_g = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
     l_g = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
     o_c = torch.empty_like(o_g)
@@ -207,10 +208,11 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     merged = torch.empty_like(o_g)
 
     def hbm():
-        ops.paged_decode(q, kc_g, vc_g, bt_g_d, len_g_d, w.scale, out=o_g, lse=l_g)
+        ops.paged_decode(q, kc_g, vc_g, bt_g_d, len_g_d, w.scale, out=o_g, lse=l_g,
+                         row_order=ord_g)
 
     def host():
-        ops.decode_attn(q, hk, hv, bt_c_d, len_c_d, w.scale, o_c, l_c)
+        ops.decode_attn(q, hk, hv, bt_c_d, len_c_d, w.scale, o_c, l_c, row_order=ord_c)
 
     def merge():
         ops.merge_attn_states(merged, o_g, l_g, o_c, l_c)
@@ -265,16 +267,19 @@ def main() -> int:
         kc, vc, _keep = cases.kv_pool(w, pool, "host", dev)
     q = cases.queries(w, dev)
     bt_d, lens_d = bt.to(dev), lens.to(dev)
+    # the planner's host-side scheduling order (rows longest first)
+    order_d = ops.longest_first(lens).to(dev)
     out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
     lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
     stream = torch.cuda.current_stream(dev)
 
     if args.layout == "vllm":
         def step():
-            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse)
+            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse,
+                             row_order=order_d)
     else:
         def step():
-            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse)
+            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse, row_order=order_d)
 
     elt = 2
     nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, elt, elt)
@@ -313,7 +318,8 @@ def main() -> int:
         "config": {
             "workload": (f"{w.name} decode attention, one layer: n={w.n}, {w.H}/{w.KVH} heads, "
                          f"D={w.D}, BS={w.BS}, L~U[{w.lo},{w.hi}], all blocks in HBM "
-                         f"({'vLLM [B,BS,KVH,2D]' if args.layout == 'vllm' else 'host [C,KVH,BS,D]'} layout)"),
+                         f"({'vLLM [B,BS,KVH,2D]' if args.layout == 'vllm' else 'host [C,KVH,BS,D]'} layout), "
+                         "rows scheduled longest-first"),
             "global_batch": w.n,
             "seq_len": w.hi,
             "parallelism": "single GPU",

@@ -93,6 +93,12 @@ int fd_abi_version(void);
  *             row's out and lse become NaN instead of reading out of bounds.
  * block_table int32 [n, >= bt_width], row stride bt_stride
  * lens        int32 [n]
+ * row_order   optional int32 [n] permutation of 0..n-1 (may be NULL): the order
+ *             in which rows are scheduled. Results do not depend on it; passing
+ *             rows longest-first shortens the launch's tail when lengths vary.
+ *             No counterpart in the reference (its planner knows every length
+ *             on the host, fastdecode/plan.py:103-199). Entries outside
+ *             [0, n) are skipped.
  * out         [n, num_heads, head_size] of out_dtype (kv_dtype or FD_F32),
  *             strides (out_stride_seq, out_stride_head, 1)
  * lse         fp32, lse[h, i] at h*lse_stride_head + i
@@ -105,7 +111,7 @@ int fd_paged_decode_partial(
     int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
     int64_t num_blocks,
     const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
-    const int32_t* lens,
+    const int32_t* lens, const int32_t* row_order,
     int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
     int32_t block_size, float scale, int32_t kv_dtype,
     void* out, int64_t out_stride_seq, int64_t out_stride_head,

@@ -71,7 +71,7 @@ def _decode(lib, **over):
     a.update(over)
     return lib.fd_paged_decode_partial(
         a["q"], a["qss"], a["qsh"], a["k"], a["v"], a["sb"], a["sh"], a["st"], a["nblk"],
-        a["bt"], a["bts"], a["btw"], a["lens"], a["n"], a["H"], a["KVH"], a["D"], a["BS"],
+        a["bt"], a["bts"], a["btw"], a["lens"], None, a["n"], a["H"], a["KVH"], a["D"], a["BS"],
         a["scale"], a["dt"], a["out"], a["oss"], a["osh"], a["odt"], a["lse"], a["lsh"],
         a["ws"], a["wsb"], None)
 

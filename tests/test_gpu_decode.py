@@ -244,3 +244,22 @@ def test_counters_left_zero_across_calls(gpu, monkeypatch):
                 if ref is None:
                     ref = out.clone()
                 assert float((out - ref).abs().max()) < 1e-5
+
+
+@pytest.mark.parametrize("name", ["correctness", "vicuna7b"])
+def test_row_order_does_not_change_results(gpu, name):
+    """Scheduling rows longest-first (or in any permutation) gives bit-identical
+    outputs; an out-of-range entry only skips its slot."""
+    w = cases.WORKLOADS[name]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    kc, vc, _keep = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    res = []
+    for order in (None, ops.longest_first(lens), torch.randperm(w.n).to(torch.int32)):
+        out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+        o, l = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out=out,
+                                row_order=order)
+        res.append((o, l))
+    torch.cuda.synchronize()
+    for o, l in res[1:]:
+        assert torch.equal(o, res[0][0]) and torch.equal(l, res[0][1])

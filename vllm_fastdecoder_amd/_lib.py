@@ -18,7 +18,7 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # name -> (restype, argtypes); the order follows include/fdattn.h
 SIGNATURES: dict[str, tuple] = {
@@ -32,7 +32,7 @@ SIGNATURES: dict[str, tuple] = {
             c_int64, c_int64, c_int64,             # kv strides block/head/token
             c_int64,                               # num_blocks
             c_void_p, c_int64, c_int32,            # block_table, bt_stride, bt_width
-            c_void_p,                              # lens
+            c_void_p, c_void_p,                    # lens, row_order
             c_int32, c_int32, c_int32, c_int32,    # n, H, KVH, D
             c_int32, c_float, c_int32,             # block_size, scale, kv_dtype
             c_void_p, c_int64, c_int64, c_int32,   # out, strides, out_dtype

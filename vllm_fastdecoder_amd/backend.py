@@ -35,16 +35,18 @@ class HipOps:
     @staticmethod
     def fa(q, k, v, cu_seqlens_q=None, max_seqlen_q=1, seqused_k=None, max_seqlen_k=None,
            softmax_scale=None, causal=False, block_table=None, softcap=0.0,
-           return_softmax_lse=False, out=None, **_):
+           return_softmax_lse=False, out=None, row_order=None, **_):
         """Paged decode partial in flash_attn_varlen_func's calling convention
         (backend.py:306-314): k/v are the [B, BS, KVH, D] cache views, one query
-        token per row, seqused_k the per-row token counts (0 allowed)."""
+        token per row, seqused_k the per-row token counts (0 allowed).
+        row_order (this build's addition) schedules rows, e.g. longest first."""
         if block_table is None or max_seqlen_q != 1 or seqused_k is None:
             raise NotImplementedError("HipOps.fa: only the paged decode form (one query "
                                       "token per row with a block table) is implemented")
         if softcap:
             raise NotImplementedError("HipOps.fa: logits soft-cap is not supported")
-        o, lse = ops.paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=out)
+        o, lse = ops.paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=out,
+                                  row_order=row_order)
         return (o, lse) if return_softmax_lse else o
 
     @staticmethod
@@ -138,6 +140,7 @@ class SplitDecodeImpl:
                     max_seqlen_q=1, seqused_k=dp.s_gpu_lens_all, max_seqlen_k=hp.s_max_gpu_len,
                     softmax_scale=self.scale, causal=False, block_table=dp.s_gpu_bt_all,
                     softcap=self.logits_soft_cap, return_softmax_lse=True, num_splits=1,
+                    row_order=dp.s_gpu_order,
                 )
             else:
                 o_gpu = torch.zeros_like(qs)
@@ -145,7 +148,7 @@ class SplitDecodeImpl:
             o_cpu = torch.empty_like(qs)
             lse_cpu = torch.empty(H, ns, dtype=torch.float32, device=qs.device)
             ops.decode_attn(qs, k_host, v_host, dp.s_cpu_bt, dp.s_cpu_lens, float(self.scale),
-                            o_cpu, lse_cpu)
+                            o_cpu, lse_cpu, row_order=dp.s_cpu_order)
 
         # 3) attention that touches no host block: P (all-HBM requests) and F
         #    (fresh prefills over this step's q/k/v) -- prefill forms of OPS.fa

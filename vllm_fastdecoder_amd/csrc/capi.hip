@@ -43,7 +43,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 1; }
+int fd_abi_version(void) { return 2; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -63,7 +63,8 @@ int fd_paged_decode_partial(const void* q, int64_t q_stride_seq, int64_t q_strid
                             const void* k_cache, const void* v_cache, int64_t kv_stride_block,
                             int64_t kv_stride_head, int64_t kv_stride_token, int64_t num_blocks,
                             const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
-                            const int32_t* lens, int32_t n, int32_t num_heads,
+                            const int32_t* lens, const int32_t* row_order, int32_t n,
+                            int32_t num_heads,
                             int32_t num_kv_heads, int32_t head_size, int32_t block_size,
                             float scale, int32_t kv_dtype, void* out, int64_t out_stride_seq,
                             int64_t out_stride_head, int32_t out_dtype, float* lse,
@@ -120,6 +121,7 @@ int fd_paged_decode_partial(const void* q, int64_t q_stride_seq, int64_t q_strid
   a.bt_stride = bt_stride;
   a.bt_width = bt_width;
   a.lens = lens;
+  a.order = row_order;
   a.n = n;
   a.H = num_heads;
   a.KVH = num_kv_heads;

@@ -155,6 +155,7 @@ struct DecodeArgs {
   int64_t bt_stride;
   int32_t bt_width;
   const int32_t* lens;
+  const int32_t* order;  // optional sequence processing order (may be NULL)
   int32_t n, H, KVH, D, BS;
   float scale;
   int32_t kv_dtype;

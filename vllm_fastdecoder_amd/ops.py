@@ -22,6 +22,7 @@ import torch
 
 from . import _lib
 from .pinned import device_ptr
+from .plan import longest_first as _longest_first
 
 _DT = {torch.float16: _lib.FD_F16, torch.bfloat16: _lib.FD_BF16, torch.float32: _lib.FD_F32}
 
@@ -93,8 +94,11 @@ def paged_decode_partial(
     out: torch.Tensor,
     lse: torch.Tensor,
     workspace: torch.Tensor | None = None,
+    row_order: torch.Tensor | None = None,
 ) -> None:
-    """Layout-generic entry: kv_strides = (block, head, token) in elements."""
+    """Layout-generic entry: kv_strides = (block, head, token) in elements.
+    row_order: optional int32 [n] permutation scheduling the rows (e.g.
+    longest_first(lens)); results do not depend on it."""
     _require(q.is_cuda and out.is_cuda and lse.is_cuda, "q, out and lse must be on the GPU")
     _require(q.dim() == 3 and out.shape == q.shape, "q and out must be [n, H, D] of one shape")
     n, H, D = q.shape
@@ -125,6 +129,12 @@ def paged_decode_partial(
         workspace = WORKSPACE.get(dev, need)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_len = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    order_ptr = None
+    if row_order is not None:
+        _require(row_order.dtype == torch.int32 and row_order.shape == (n,),
+                 "row_order must be int32 [n]")
+        row_order = _on_device(row_order, dev).contiguous()
+        order_ptr = row_order.data_ptr()
     lib = _lib.load_lib()
     _lib.check(
         lib.fd_paged_decode_partial(
@@ -133,7 +143,7 @@ def paged_decode_partial(
             kv_strides[0], kv_strides[1], kv_strides[2],
             num_blocks,
             bt.data_ptr(), bt.stride(0), W,
-            ln.data_ptr(),
+            ln.data_ptr(), order_ptr,
             n, H, num_kv_heads, D,
             block_size, float(scale), kv_dt,
             out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
@@ -144,12 +154,19 @@ def paged_decode_partial(
     )
 
 
-def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse) -> None:
+def longest_first(lens: torch.Tensor) -> torch.Tensor:
+    """int32 permutation of the rows by decreasing length, computed on the
+    host (the planner already holds the lengths there)."""
+    return _longest_first(lens.cpu())
+
+
+def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse, row_order=None) -> None:
     """Host-tier layout partial, signature of cpu_attn.cpp:456-489.
 
     q [n, H, D]; k_cache/v_cache [C, KVH, BS, D] (pinned host memory or HBM);
     block_table [n, W] int32 (tier-relative ids in sequence order); lens [n]
     int32; out [n, H, D] (q's dtype, or float32); lse [H, n] float32.
+    row_order: optional scheduling permutation (this build's addition).
     """
     _require(k_cache.dim() == 4 and v_cache.shape == k_cache.shape,
              "k_cache/v_cache must be [C, KVH, BS, D]")
@@ -159,7 +176,7 @@ def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse) -> None
     _require(k_cache.stride(3) == 1, "k_cache must be contiguous in head_size")
     paged_decode_partial(
         q, k_cache, v_cache, (k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)),
-        C, BS, KVH, block_table, lens, scale, out, lse,
+        C, BS, KVH, block_table, lens, scale, out, lse, row_order=row_order,
     )
 
 
@@ -172,6 +189,7 @@ def paged_decode(
     softmax_scale: float,
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
+    row_order: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """HBM-tier partial in vLLM's paged layout: the decode call of
     flash_attn_varlen_func at fastdecode/backend.py:306-314 (one query token
@@ -194,7 +212,7 @@ def paged_decode(
     paged_decode_partial(
         q, key_cache, value_cache,
         (key_cache.stride(0), key_cache.stride(2), key_cache.stride(1)),
-        B, BS, KVH, block_table, seqused_k, softmax_scale, out, lse,
+        B, BS, KVH, block_table, seqused_k, softmax_scale, out, lse, row_order=row_order,
     )
     return out, lse
 

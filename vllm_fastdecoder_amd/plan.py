@@ -230,6 +230,14 @@ class DevicePlan:
     s_cpu_bt: torch.Tensor | None = None  # [nS, Wc] int32
     s_cpu_lens: torch.Tensor | None = None  # [nS] int32
     host_slot_mapping: torch.Tensor | None = None  # [n_tok] int64
+    # scheduling order of the S rows for each tier's partial: longest first
+    s_gpu_order: torch.Tensor | None = None  # [nS] int32
+    s_cpu_order: torch.Tensor | None = None  # [nS] int32
+
+
+def longest_first(lens: torch.Tensor) -> torch.Tensor:
+    """int32 row permutation by decreasing length (stable)."""
+    return torch.argsort(lens.to(torch.int64), descending=True, stable=True).to(torch.int32)
 
 
 def to_device(hp: HostPlan, block_table_dev: torch.Tensor, device) -> DevicePlan:
@@ -258,4 +266,6 @@ def to_device(hp: HostPlan, block_table_dev: torch.Tensor, device) -> DevicePlan
         s_cpu_bt=d(hp.s_cpu_bt),
         s_cpu_lens=d(hp.s_cpu_lens),
         host_slot_mapping=d(hp.host_slot_mapping) if hp.host_slot_mapping is not None else None,
+        s_gpu_order=d(longest_first(hp.s_gpu_lens)),
+        s_cpu_order=d(longest_first(hp.s_cpu_lens)),
     )
