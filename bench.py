@@ -45,8 +45,8 @@ METRIC = "split decode-attn achieved HBM GB/s (% of peak) + tokens/s, vicuna-7b 
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--workload", default="vicuna7b", choices=["vicuna7b", "llama3_8b", "correctness"])
     ap.add_argument("--layout", default="vllm", choices=["vllm", "host"])
     ap.add_argument("--no-cpu-baseline", action="store_true")

@@ -218,6 +218,64 @@ def test_full_size_workloads_match_oracle(gpu, name):
     assert_lse_close(l, ref_lse)
 
 
+GQA_LENS = [0, 1, 15, 16, 17, 93, 160, 47]
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("G", [4, 8])
+def test_gqa_kernels_match_oracle(gpu, kernel, dtype, D, G, monkeypatch):
+    """Grouped-query rows (G = 4, 8) on the matrix-core kernel (default) and on
+    the VALU kernel (FD_DECODE_KERNEL=valu): lengths 0, 1, a partial block,
+    exactly one block, one token past it; whole rows and forced 2-block splits."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    KVH = 2
+    H = G * KVH
+    n, BS, C = len(GQA_LENS), 16, 96
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=160, seed=D * G)
+    lens[:] = torch.tensor(GQA_LENS, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, torch.float32, gpu)
+        assert_out_close(out, ref_out, 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+        out16, lse16 = run_host_layout(q, kc, vc, bt, lens, scale, dtype, gpu)
+        tol = OUT_TOL_16BIT[dtype]
+        assert_out_close(out16, ref_out, tol, tol, mask=nz)
+        assert torch.equal(lse16, lse)
+
+
+def test_gqa_large_scores_and_range_errors(gpu):
+    """Matrix-core kernel: q x 300 stays finite and exact to the oracle; a bad
+    table entry or an over-long length poisons only its own row."""
+    n, H, KVH, D, BS, C = 4, 16, 4, 128, 16, 16
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float32, 64, 9)
+    q16 = (q * 300.0).to(torch.bfloat16)
+    kc, vc = kc.to(torch.bfloat16), vc.to(torch.bfloat16)
+    lens[:] = torch.tensor([64, 40, 33, 17], dtype=torch.int32)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q16, kc, vc, bt, lens, 1.0)
+    out, lse = run_host_layout(q16, kc, vc, bt, lens, 1.0, torch.float32, gpu)
+    assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+    assert_out_close(out, ref_out, 1e-3)
+    assert float((lse.double().cpu() - ref_lse).abs().max()) <= 1e-3 * float(ref_lse.abs().max())
+    bt_bad = bt.clone()
+    bt_bad[1, 1] = C + 5  # past the cache
+    lens_bad = lens.clone()
+    lens_bad[2] = bt.shape[1] * BS + 1  # beyond the table
+    out, lse = run_host_layout(q16, kc, vc, bt_bad, lens_bad, 1.0, torch.float32, gpu)
+    assert torch.isnan(out[1]).all() and torch.isnan(lse[:, 1]).all()
+    assert torch.isnan(out[2]).all() and torch.isnan(lse[:, 2]).all()
+    ok = torch.tensor([True, False, False, True])
+    assert_out_close(out, ref_out, 1e-3, mask=ok)
+
+
 @pytest.mark.skip(reason="covers the persistent work-queue decode kernel, which faulted the GPU "
                          "on its first run with no cause found by reading; that code path was "
                          "removed, so this test has nothing to run against")

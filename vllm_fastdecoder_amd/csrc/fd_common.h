@@ -25,6 +25,10 @@ inline int dtype_size(int dt) {
 // ---------------------------------------------------------------- types
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf162_t __attribute__((ext_vector_type(2)));
+// matrix-core operand / accumulator vectors
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Storage tags for 16-bit KV elements. Both are moved around as raw 16-bit
 // words; only the arithmetic below differs.
@@ -119,6 +123,14 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// Max over aligned groups of 16 lanes (one DPP row); every lane receives it.
+__device__ __forceinline__ float row_max16(float x) {
+  x = fmaxf(x, dpp<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
+  return fmaxf(x, dpp<kDppRowMirror>(x));
+}
+
 __device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
   return __shfl_xor(x, mask, kWave);
 }
@@ -173,6 +185,8 @@ struct SplitPlan {
   int32_t split_blocks;  // blocks handled by one wavefront task
   int32_t max_splits;    // ceil(bt_width / split_blocks)
   bool fast;             // the tiled kernel applies (else the generic one)
+  bool mfma;             // grouped-query scores on the matrix cores (G >= 4)
+  bool cap_occupancy;    // long tasks: at most two workgroups per CU
 };
 
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
