@@ -161,7 +161,8 @@ def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
 
 def split_run(w, lens, bt, q, steps, warmup, stream):
     """60% of each row's blocks (the last ones) in pinned host memory, the rest
-    in HBM: HBM partial + host partial (zero-copy) + LSE merge."""
+    in HBM: HBM partial + host partial (zero-copy) + LSE merge, and the same
+    step as one fused launch (ops.split_decode)."""
     import torch
 
     from tests import cases
@@ -222,11 +223,20 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         host()
         merge()
 
+    ord_all = ops.longest_first(len_g + len_c).to(dev)
+    f_out = torch.empty_like(o_g)
+    f_lse = torch.empty_like(l_g)
+
+    def fused():
+        ops.split_decode(q, kc_g, vc_g, bt_g_d, len_g_d, hk, hv, bt_c_d, len_c_d, w.scale,
+                         out=f_out, lse=f_lse, row_order=ord_all)
+
     host_steps = max(2, min(steps, 5))
     t_hbm = time_gpu(hbm, steps, warmup, stream)
     t_host = time_gpu(host, host_steps, 1, stream)
     t_merge = time_gpu(merge, steps, warmup, stream)
     t_step = time_gpu(step, host_steps, 1, stream)
+    t_fused = time_gpu(fused, host_steps, 1, stream)
     b_hbm, kv_hbm = algorithmic_bytes(len_g, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     b_host, kv_host = algorithmic_bytes(len_c, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     del kv, hk, hv
@@ -239,6 +249,8 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "merge_ms": round(t_merge, 4),
         "step_ms": round(t_step, 3),
         "step_tokens_per_s": round(w.n / (t_step / 1e3 * LAYERS), 1),
+        "fused_step_ms": round(t_fused, 3),
+        "fused_step_tokens_per_s": round(w.n / (t_fused / 1e3 * LAYERS), 1),
         "note": "host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not `value`",
     }
 

@@ -128,6 +128,52 @@ int fd_paged_decode_workspace_size(
     int32_t block_size, int32_t bt_width, size_t* bytes);
 
 /* ------------------------------------------------------------------------
+ * Fused split decode: both tiers of a row in one launch.
+ *
+ * Replaces the three calls of the reference's split-decode step
+ * (fastdecode/backend.py:293-356): the GPU-tier FlashAttention partial
+ * (:305-316), the host-tier decode_attn partial (:350-351) and
+ * merge_attn_states (:354-355). For every sequence i and query head h the
+ * result is attention over the union of the row's two block lists,
+ *   out[i, h, :] = softmax(scale * q . [K_hbm ; K_host]^T) @ [V_hbm ; V_host]
+ *   lse[h, i]    = logsumexp over both tiers (natural log),
+ * which equals merge(partial_hbm, partial_host) of the separate calls. The
+ * kernel walks each row's HBM-tier blocks, then its host-tier blocks, as one
+ * list and merges in-kernel: no partial round trip and no merge launch.
+ *
+ * Each tier is described by an fd_kv_tier: the same cache/stride/table/length
+ * conventions as fd_paged_decode_partial, per tier (tier-relative block ids,
+ * as the reference's planner produces them: s_gpu_bt / s_gpu_lens and
+ * s_cpu_bt / s_cpu_lens, fastdecode/plan.py:160-172). A row with no tokens in
+ * either tier yields out = 0, lse = -inf; a range error in either tier makes
+ * the row NaN. The host tier's caches may be mapped pinned host memory.
+ * workspace: >= fd_paged_decode_workspace_size(n, ..., hbm->bt_width +
+ * host->bt_width) bytes. No counterpart as a single call in the reference.
+ * ------------------------------------------------------------------------ */
+typedef struct fd_kv_tier {
+  const void* k_cache;
+  const void* v_cache;
+  int64_t stride_block, stride_head, stride_token; /* elements */
+  int64_t num_blocks;
+  const int32_t* block_table; /* int32 [n, >= bt_width], row stride bt_stride */
+  int64_t bt_stride;
+  int32_t bt_width;
+  const int32_t* lens; /* int32 [n]: tokens of each row held in this tier */
+} fd_kv_tier;
+
+int fd_split_decode(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const fd_kv_tier* hbm, const fd_kv_tier* host,
+    const int32_t* row_order,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* ------------------------------------------------------------------------
  * Log-sum-exp merge of two partials.
  *
  * Replaces vLLM's merge_attn_states(out, o_a, lse_a, o_b, lse_b) called at

@@ -147,17 +147,21 @@ def decode_attn_cpu_f32(q, k_cache, v_cache, block_table, lens, scale, out, lse,
         out.data_ptr(), lse.data_ptr(), threads)
 
 
+_DT_MERGE = {**_DT, torch.float64: 3}
+
+
 def merge_f64(o_a, lse_a, o_b, lse_b):
-    """float64 LSE merge (cpu_ops.py:93-113). Returns (out [n,H,D], lse [H,n])."""
+    """float64 LSE merge (cpu_ops.py:93-113) of partials in fp16/bf16/fp32 or
+    float64 (the oracle's own). Returns (out [n,H,D], lse [H,n])."""
     o_a = _cpu(o_a).contiguous()
     o_b = _cpu(o_b).contiguous()
-    la = _cpu(lse_a).float().contiguous()
-    lb = _cpu(lse_b).float().contiguous()
+    la = _cpu(lse_a).double().contiguous()
+    lb = _cpu(lse_b).double().contiguous()
     n, H, D = o_a.shape
     out = torch.empty(n, H, D, dtype=torch.float64)
     olse = torch.empty(H, n, dtype=torch.float64)
-    lib().oracle_merge_f64(o_a.data_ptr(), _DT[o_a.dtype], la.data_ptr(), o_b.data_ptr(),
-                           _DT[o_b.dtype], lb.data_ptr(), n, H, D, out.data_ptr(),
+    lib().oracle_merge_f64(o_a.data_ptr(), _DT_MERGE[o_a.dtype], la.data_ptr(), o_b.data_ptr(),
+                           _DT_MERGE[o_b.dtype], lb.data_ptr(), n, H, D, out.data_ptr(),
                            olse.data_ptr())
     return out, olse
 

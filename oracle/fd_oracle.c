@@ -83,7 +83,13 @@ static inline float load_f(const void* p, int64_t i, int dt) {
   return dt == 0 ? half_to_float(w) : bf16_to_float(w);
 }
 
-int oracle_elem_size(int dt) { return dt == 2 ? 4 : 2; }
+/* Merge inputs may also be float64 (dt 3): the oracle's own partials. */
+static inline double load_d(const void* p, int64_t i, int dt) {
+  if (dt == 3) return ((const double*)p)[i];
+  return (double)load_f(p, i, dt);
+}
+
+int oracle_elem_size(int dt) { return dt == 3 ? 8 : dt == 2 ? 4 : 2; }
 
 /* Converts n elements of dtype dt to float (helper for tests). */
 void oracle_to_float(const void* src, int dt, int64_t n, float* dst) {
@@ -258,9 +264,10 @@ void oracle_decode_attn_cpu_f32(const void* q, const void* kc, const void* vc,
 
 /* out[i,h,:] = o_a * w_a + o_b * w_b in float64 with the torch rule:
  * +inf lse -> -inf; both empty -> m = 0, weights' sum = 1 (out = 0).
- * o_* [n, H, D] contiguous of dtype a_dt / b_dt; lse_* float [H, n]. */
-void oracle_merge_f64(const void* o_a, int a_dt, const float* lse_a, const void* o_b, int b_dt,
-                      const float* lse_b, int n, int H, int D, double* out, double* out_lse) {
+ * o_* [n, H, D] contiguous of dtype a_dt / b_dt (fp16, bf16, fp32 or
+ * float64); lse_* float64 [H, n]. */
+void oracle_merge_f64(const void* o_a, int a_dt, const double* lse_a, const void* o_b, int b_dt,
+                      const double* lse_b, int n, int H, int D, double* out, double* out_lse) {
   for (int i = 0; i < n; ++i) {
     for (int h = 0; h < H; ++h) {
       double la = lse_a[(int64_t)h * n + i], lb = lse_b[(int64_t)h * n + i];
@@ -274,7 +281,7 @@ void oracle_merge_f64(const void* o_a, int a_dt, const float* lse_a, const void*
       const double wa = wa0 / tot, wb = wb0 / tot;
       const int64_t base = ((int64_t)i * H + h) * D;
       for (int d = 0; d < D; ++d)
-        out[base + d] = load_f(o_a, base + d, a_dt) * wa + load_f(o_b, base + d, b_dt) * wb;
+        out[base + d] = load_d(o_a, base + d, a_dt) * wa + load_d(o_b, base + d, b_dt) * wb;
       if (out_lse) out_lse[(int64_t)h * n + i] = both_empty ? -INFINITY : m + log(tot);
     }
   }

@@ -118,3 +118,54 @@ def test_merge_and_cache_write_reject_bad_arguments():
                                     16, 0, None, None) == _lib.FD_ERR_INVALID
     assert lib.fd_stream_copy(16, 16, 17, None) == _lib.FD_ERR_INVALID
     assert lib.fd_host_device_pointer(None, None) == _lib.FD_ERR_INVALID
+
+
+def _tier(**over):
+    t = dict(k=32, v=48, sb=4 * 16 * 64, sh=16 * 64, st=64, nblk=10, bt=64, bts=4, btw=4, lens=80)
+    t.update(over)
+    return _lib.FdKvTier(t["k"], t["v"], t["sb"], t["sh"], t["st"], t["nblk"], t["bt"], t["bts"],
+                         t["btw"], t["lens"])
+
+
+def _split(lib, hbm=None, host=None, **over):
+    """fd_split_decode with plausible pointers (never dereferenced: every call
+    here must be rejected by host validation, or be a no-op)."""
+    a = dict(q=16, qss=8 * 64, qsh=64, n=2, H=8, KVH=4, D=64, BS=16, scale=0.125, dt=0,
+             out=96, oss=8 * 64, osh=64, odt=0, lse=112, lsh=2, ws=None, wsb=0)
+    a.update(over)
+    th = hbm if hbm is not None else _tier()
+    tc = host if host is not None else _tier()
+    return lib.fd_split_decode(
+        a["q"], a["qss"], a["qsh"], ctypes.byref(th), ctypes.byref(tc), None, a["n"], a["H"],
+        a["KVH"], a["D"], a["BS"], a["scale"], a["dt"], a["out"], a["oss"], a["osh"], a["odt"],
+        a["lse"], a["lsh"], a["ws"], a["wsb"], None)
+
+
+@pytest.mark.parametrize(
+    "tiers,over,code",
+    [
+        (dict(host=_tier(bts=2)), {}, _lib.FD_ERR_INVALID),       # host row stride < width
+        (dict(host=_tier(lens=None)), {}, _lib.FD_ERR_INVALID),   # host lens missing
+        (dict(hbm=_tier(k=None)), {}, _lib.FD_ERR_INVALID),       # hbm cache missing
+        (dict(host=_tier(nblk=-1)), {}, _lib.FD_ERR_INVALID),
+        ({}, dict(H=6, KVH=4), _lib.FD_ERR_INVALID),
+        ({}, dict(odt=1), _lib.FD_ERR_INVALID),
+        # the two tables together are what a task splits over: 128 + 128 blocks
+        # of 2 rows split, and the split partials need workspace
+        (dict(hbm=_tier(btw=128, bts=128), host=_tier(btw=128, bts=128)), {},
+         _lib.FD_ERR_WORKSPACE),
+    ],
+)
+def test_split_decode_rejects_bad_arguments_on_host(tiers, over, code):
+    lib = _lib.load_lib()
+    assert _split(lib, **tiers, **over) == code
+    assert lib.fd_last_error()
+
+
+def test_split_decode_null_descriptor_and_n_zero():
+    lib = _lib.load_lib()
+    t = _tier()
+    assert lib.fd_split_decode(16, 512, 64, None, ctypes.byref(t), None, 2, 8, 4, 64, 16, 0.125,
+                               0, 96, 512, 64, 0, 112, 2, None, 0, None) == _lib.FD_ERR_INVALID
+    # n == 0: nothing to do, even with NULL tier pointers
+    assert _split(lib, hbm=_tier(k=None, lens=None), host=_tier(bt=None), n=0) == _lib.FD_OK

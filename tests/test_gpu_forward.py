@@ -128,10 +128,13 @@ REQS16 = [
 ]
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("case", ["reqs4", "reqs16"])
 @pytest.mark.parametrize("H,KVH", [(4, 4), (8, 2)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH, dtype):
+def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH, dtype, fused):
+    """S rows through the fused launch (default) or the reference's two
+    partials + merge; P and F rows as in the reference."""
     if case == "reqs4":
         reqs, G, C, BS, D = KATS["classification"]["reqs"], 10, 20, 4, 64
     else:
@@ -140,7 +143,7 @@ def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH,
     hp = plan.build_host_plan(sc.qsl, sc.seq, sc.bt, sc.slots, G, C, BS)
     dp = plan.to_device(hp, sc.bt.to(gpu), gpu)
     state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k}, v={"l0": sc.host_v})
-    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale)
+    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, fused_split=fused)
     layer = SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None)
     output = torch.full_like(sc.query, float("nan"))
     impl._forward_split(layer, sc.query, sc.key, sc.value, sc.kv_cache, dp, output)
@@ -194,15 +197,17 @@ def test_hipops_fa_rejects_prefill_forms(gpu):
                           softmax_scale=0.1, causal=True)
 
 
-def test_continuous_batching_simulation(gpu):
+@pytest.mark.parametrize("fused", [True, False])
+def test_continuous_batching_simulation(gpu, fused):
     """The config of the reference's GPU self-test at vicuna-7b head shapes:
     300 decode steps, G=256 HBM blocks, C=2048 host blocks, Poisson(4)
     arrivals, prompts U[64,512], outputs U[32,512], GPU-first allocation with
     block reuse; every step checked against monolithic attention over one
-    G+C pool written with the same KV, and every slot written bit-exact."""
+    G+C pool written with the same KV, and every slot written bit-exact. S
+    rows through the fused launch and through two partials + merge."""
     from tests.simulate import run_simulation
 
-    stats = run_simulation(steps=300, seed=4, device=gpu)
+    stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
     assert stats["split_steps"] > 100 and stats["decode_rows"] > 1000

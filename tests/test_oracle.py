@@ -244,6 +244,10 @@ def test_split_and_merge_equals_monolithic():
     merged, mlse = oracle.merge_f64(oa.float(), lsa.float(), ob.float(), lsb.float())
     torch.testing.assert_close(merged, full, atol=1e-6, rtol=0)
     torch.testing.assert_close(mlse, full_lse, atol=1e-5, rtol=0)
+    # float64 partials merge to the float64 whole up to float64 rounding
+    merged, mlse = oracle.merge_f64(oa, lsa, ob, lsb)
+    torch.testing.assert_close(merged, full, atol=1e-12, rtol=0)
+    torch.testing.assert_close(mlse, full_lse, atol=1e-12, rtol=0)
     # planted mistake: merging with unnormalised weights must be caught
     wrong = oa.double() * torch.exp(lsa.double()).t().unsqueeze(-1) + ob.double() * torch.exp(lsb.double()).t().unsqueeze(-1)
     assert float((wrong - full).abs().max()) > 2e-3

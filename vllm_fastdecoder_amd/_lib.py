@@ -18,7 +18,25 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 2
+ABI_VERSION = 3
+
+
+class FdKvTier(ctypes.Structure):
+    """struct fd_kv_tier of include/fdattn.h: one KV tier of fd_split_decode."""
+
+    _fields_ = [
+        ("k_cache", c_void_p),
+        ("v_cache", c_void_p),
+        ("stride_block", c_int64),
+        ("stride_head", c_int64),
+        ("stride_token", c_int64),
+        ("num_blocks", c_int64),
+        ("block_table", c_void_p),
+        ("bt_stride", c_int64),
+        ("bt_width", c_int32),
+        ("lens", c_void_p),
+    ]
+
 
 # name -> (restype, argtypes); the order follows include/fdattn.h
 SIGNATURES: dict[str, tuple] = {
@@ -44,6 +62,20 @@ SIGNATURES: dict[str, tuple] = {
     "fd_paged_decode_workspace_size": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_size_t)],
+    ),
+    "fd_split_decode": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64,            # q, q strides
+            POINTER(FdKvTier), POINTER(FdKvTier),  # hbm tier, host tier
+            c_void_p,                              # row_order
+            c_int32, c_int32, c_int32, c_int32,    # n, H, KVH, D
+            c_int32, c_float, c_int32,             # block_size, scale, kv_dtype
+            c_void_p, c_int64, c_int64, c_int32,   # out, strides, out_dtype
+            c_void_p, c_int64,                     # lse, lse_stride_head
+            c_void_p, c_size_t,                    # workspace
+            c_void_p,                              # stream
+        ],
     ),
     "fd_merge_attn_states": (
         c_int,

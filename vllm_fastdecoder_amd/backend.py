@@ -7,8 +7,9 @@ vLLM's base classes:
     `merge`, `event`), routed to libfdattn. `fa` implements the paged decode
     form the split path uses (one query token per row, block table,
     return_softmax_lse); prefill forms raise NotImplementedError (FlashAttention
-    prefill is not on this path). Tests swap OPS the way the reference's tests
-    do (tests/test_plan_and_forward.py:106-113).
+    prefill is not on this path). `split_decode` (this build's addition) is
+    the fused form of the S rows' two partials and their merge. Tests swap
+    OPS the way the reference's tests do (tests/test_plan_and_forward.py:106-113).
   * `build_split_plan` -- FastDecodeMetadataBuilder.build (backend.py:140-178):
     one device-to-host copy of the step's block table and slots, the host
     planner, then the device plan.
@@ -48,6 +49,15 @@ class HipOps:
         o, lse = ops.paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=out,
                                   row_order=row_order)
         return (o, lse) if return_softmax_lse else o
+
+    @staticmethod
+    def split_decode(q, key_cache, value_cache, gpu_block_table, gpu_lens, host_k_cache,
+                     host_v_cache, host_block_table, host_lens, softmax_scale, row_order=None):
+        """Both tiers of every S row in one launch: the result of the GPU-tier
+        partial, the host-tier partial and their merge (backend.py:293-356)."""
+        return ops.split_decode(q, key_cache, value_cache, gpu_block_table, gpu_lens,
+                                host_k_cache, host_v_cache, host_block_table, host_lens,
+                                softmax_scale, row_order=row_order)
 
     @staticmethod
     def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, kv_cache_dtype="auto",
@@ -102,6 +112,9 @@ class SplitDecodeImpl:
     kv_cache_dtype: str = "auto"
     logits_soft_cap: float = 0.0
     kv_sharing_target_layer_name: str | None = None
+    # S rows through one fused launch (OPS.split_decode) instead of two
+    # partials and a merge; the unfused path is the reference's contract
+    fused_split: bool = True
 
     def _forward_split(self, layer, query, key, value, kv_cache, dp: DevicePlan, output):
         """query [T, H, D]; key/value [T, KVH, D] (possibly strided views);
@@ -127,11 +140,17 @@ class SplitDecodeImpl:
                 vw = value.index_select(0, dp.cpu_w_tok)
                 ops.store_kv(kw, vw, hp.cpu_w_slot, k_host, v_host)
 
-        # 2) split decodes: HBM-tier and host-tier partials, both on the GPU.
-        #    Rows without HBM tokens come back as (0, -inf) from the kernel, so
-        #    every S row goes in as is.
+        # 2) split decodes: HBM-tier and host-tier partials, both on the GPU
+        #    (or both tiers in one fused launch). Rows without HBM tokens come
+        #    back as (0, -inf) from the kernel, so every S row goes in as is.
         ns = hp.n_s
-        if ns:
+        fused = self.fused_split and getattr(OPS, "split_decode", None) is not None
+        if ns and fused:
+            qs = query.index_select(0, dp.s_tok)
+            merged, _ = OPS.split_decode(qs, key_cache, value_cache, dp.s_gpu_bt_all,
+                                         dp.s_gpu_lens_all, k_host, v_host, dp.s_cpu_bt,
+                                         dp.s_cpu_lens, float(self.scale), row_order=dp.s_order)
+        elif ns:
             qs = query.index_select(0, dp.s_tok)
             if hp.s_max_gpu_len > 0:
                 o_gpu, lse_gpu = fa(
@@ -173,7 +192,8 @@ class SplitDecodeImpl:
 
         # 4) merge the split decodes' partials into their output rows
         if ns:
-            merged = torch.empty_like(qs)
-            OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
+            if not fused:
+                merged = torch.empty_like(qs)
+                OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
             output.index_copy_(0, dp.s_tok, merged)
         return output

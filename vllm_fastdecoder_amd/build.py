@@ -9,6 +9,8 @@ from __future__ import annotations
 
 import os
 import subprocess
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -22,7 +24,6 @@ HIPCC_FLAGS = [
     "-std=c++17",
     f"--offload-arch={ARCH}",
     "-fPIC",
-    "-shared",
     # keep packed-fp32 VALU ops out of the generated code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
@@ -40,11 +41,7 @@ def hipcc() -> str:
     return str(cand) if cand.exists() else "hipcc"
 
 
-def build(verbose: bool = False, out: Path | None = None) -> Path:
-    """Compiles every csrc/*.hip into one shared library (always rebuilds)."""
-    out = out or LIB_PATH
-    tmp = out.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, *map(str, sources()), "-o", str(tmp)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -55,6 +52,24 @@ def build(verbose: bool = False, out: Path | None = None) -> Path:
         lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
         if lines:
             print("\n".join(lines))
+
+
+def build(verbose: bool = False, out: Path | None = None) -> Path:
+    """Compiles every csrc/*.hip (one hipcc per source, in parallel) and links
+    them into one shared library. Always rebuilds."""
+    out = out or LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
+    srcs = sources()
+    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with tempfile.TemporaryDirectory(prefix="fdattn_build_") as d:
+        objs = [Path(d) / (src.stem + ".o") for src in srcs]
+        cmds = [[hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+                for src, obj in zip(srcs, objs)]
+        with ThreadPoolExecutor(max_workers=jobs) as pool:
+            for f in [pool.submit(_run, c, verbose) for c in cmds]:
+                f.result()
+        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", *map(str, objs),
+              "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

@@ -34,6 +34,85 @@ bool valid_dtype(int dt) { return dt == FD_F16 || dt == FD_BF16 || dt == FD_F32;
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Validates a decode call over a.ntiers tiers (tiers already filled in),
+// completes `a` and launches it. Every check runs before the launch.
+int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_seq,
+               int64_t q_stride_head, const int32_t* row_order, int32_t n, int32_t num_heads,
+               int32_t num_kv_heads, int32_t head_size, int32_t block_size, float scale,
+               int32_t kv_dtype, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+               int32_t out_dtype, float* lse, int64_t lse_stride_head, void* workspace,
+               size_t workspace_bytes, void* stream) {
+  if (n < 0) return set_error(FD_ERR_INVALID, "%s: n must be >= 0 (got %d)", who, n);
+  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return set_error(FD_ERR_INVALID,
+                     "%s: num_heads must be a multiple of num_kv_heads (%d, %d)", who, num_heads,
+                     num_kv_heads);
+  if (head_size <= 0 || head_size > 512)
+    return set_error(FD_ERR_UNSUPPORTED, "%s: head_size %d outside 1..512", who, head_size);
+  if (block_size <= 0) return set_error(FD_ERR_INVALID, "%s: block_size must be > 0", who);
+  if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "%s: unsupported kv dtype %d", who, kv_dtype);
+  if (out_dtype != kv_dtype && out_dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "%s: out dtype must equal the kv dtype or be fp32", who);
+  if (!std::isfinite(scale)) return set_error(FD_ERR_INVALID, "%s: scale is not finite", who);
+  int64_t width = 0;
+  for (int t = 0; t < a.ntiers; ++t) {
+    if (a.tier[t].bt_width < 0 || a.tier[t].num_blocks < 0)
+      return set_error(FD_ERR_INVALID, "%s: negative size (tier %d)", who, t);
+    width += a.tier[t].bt_width;
+  }
+  if (width > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "%s: table too wide", who);
+  if (n == 0) return FD_OK;
+  if (!q || !out || !lse) return set_error(FD_ERR_INVALID, "%s: NULL tensor pointer", who);
+  for (int t = 0; t < a.ntiers; ++t) {
+    const KvTier& kt = a.tier[t];
+    if (!kt.k || !kt.v || !kt.bt || !kt.lens)
+      return set_error(FD_ERR_INVALID, "%s: NULL tensor pointer (tier %d)", who, t);
+    if (kt.bt_width > 0 && kt.bt_stride < kt.bt_width)
+      return set_error(FD_ERR_INVALID, "%s: bt_stride %lld < bt_width %d (tier %d)", who,
+                       (long long)kt.bt_stride, kt.bt_width, t);
+  }
+
+  // An empty cache goes to the generic kernel, which never reads it.
+  bool aligned = aligned16(q) && aligned16(out) && q_stride_seq % 8 == 0 &&
+                 q_stride_head % 8 == 0 && out_stride_seq % 8 == 0 && out_stride_head % 8 == 0;
+  for (int t = 0; t < a.ntiers; ++t) {
+    const KvTier& kt = a.tier[t];
+    aligned = aligned && kt.num_blocks > 0 && aligned16(kt.k) && aligned16(kt.v) &&
+              kt.sb % 8 == 0 && kt.sh % 8 == 0 && kt.st % 8 == 0 &&
+              // one (block, head) run must be addressable by a 32-bit offset
+              ((int64_t)(block_size - 1) * kt.st + head_size) * 2 < (1ll << 31);
+  }
+  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
+                                   (int32_t)width, kv_dtype, aligned);
+  const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+    return set_error(FD_ERR_WORKSPACE,
+                     "%s: workspace of %zu bytes (16-byte aligned) required, got %zu", who, need,
+                     workspace == nullptr ? (size_t)0 : workspace_bytes);
+
+  a.q = q;
+  a.q_ss = q_stride_seq;
+  a.q_sh = q_stride_head;
+  a.order = row_order;
+  a.n = n;
+  a.H = num_heads;
+  a.KVH = num_kv_heads;
+  a.D = head_size;
+  a.BS = block_size;
+  a.scale = scale;
+  a.kv_dtype = kv_dtype;
+  a.out = out;
+  a.out_ss = out_stride_seq;
+  a.out_sh = out_stride_head;
+  a.out_dtype = out_dtype;
+  a.lse = lse;
+  a.lse_sh = lse_stride_head;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return launch_decode(a, sp, static_cast<hipStream_t>(stream));
+}
+
 }  // namespace
 }  // namespace fd
 
@@ -43,7 +122,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 2; }
+int fd_abi_version(void) { return 3; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -70,74 +149,37 @@ int fd_paged_decode_partial(const void* q, int64_t q_stride_seq, int64_t q_strid
                             int64_t out_stride_head, int32_t out_dtype, float* lse,
                             int64_t lse_stride_head, void* workspace, size_t workspace_bytes,
                             void* stream) {
-  if (n < 0) return set_error(FD_ERR_INVALID, "decode: n must be >= 0 (got %d)", n);
-  if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
-    return set_error(FD_ERR_INVALID,
-                     "decode: num_heads must be a multiple of num_kv_heads (%d, %d)", num_heads,
-                     num_kv_heads);
-  if (head_size <= 0 || head_size > 512)
-    return set_error(FD_ERR_UNSUPPORTED, "decode: head_size %d outside 1..512", head_size);
-  if (block_size <= 0) return set_error(FD_ERR_INVALID, "decode: block_size must be > 0");
-  if (bt_width < 0 || num_blocks < 0) return set_error(FD_ERR_INVALID, "decode: negative size");
-  if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
-    return set_error(FD_ERR_INVALID, "decode: unsupported kv dtype %d", kv_dtype);
-  if (out_dtype != kv_dtype && out_dtype != FD_F32)
-    return set_error(FD_ERR_INVALID, "decode: out dtype must equal the kv dtype or be fp32");
-  if (!std::isfinite(scale)) return set_error(FD_ERR_INVALID, "decode: scale is not finite");
-  if (n == 0) return FD_OK;
-  if (!q || !k_cache || !v_cache || !block_table || !lens || !out || !lse)
-    return set_error(FD_ERR_INVALID, "decode: NULL tensor pointer");
-  if (bt_width > 0 && bt_stride < bt_width)
-    return set_error(FD_ERR_INVALID, "decode: bt_stride %lld < bt_width %d",
-                     (long long)bt_stride, bt_width);
-
-  // An empty cache goes to the generic kernel, which never reads it.
-  const bool aligned = num_blocks > 0 && aligned16(q) && aligned16(k_cache) && aligned16(v_cache) &&
-                       aligned16(out) && q_stride_seq % 8 == 0 && q_stride_head % 8 == 0 &&
-                       kv_stride_block % 8 == 0 && kv_stride_head % 8 == 0 &&
-                       kv_stride_token % 8 == 0 && out_stride_seq % 8 == 0 &&
-                       out_stride_head % 8 == 0 &&
-                       // one (block, head) run must be addressable by a 32-bit offset
-                       ((int64_t)(block_size - 1) * kv_stride_token + head_size) * 2 < (1ll << 31);
-  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
-                                   bt_width, kv_dtype, aligned);
-  const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
-    return set_error(FD_ERR_WORKSPACE,
-                     "decode: workspace of %zu bytes (16-byte aligned) required, got %zu", need,
-                     workspace == nullptr ? (size_t)0 : workspace_bytes);
-
   DecodeArgs a{};
-  a.q = q;
-  a.q_ss = q_stride_seq;
-  a.q_sh = q_stride_head;
-  a.k = k_cache;
-  a.v = v_cache;
-  a.kv_sb = kv_stride_block;
-  a.kv_sh = kv_stride_head;
-  a.kv_st = kv_stride_token;
-  a.num_blocks = num_blocks;
-  a.bt = block_table;
-  a.bt_stride = bt_stride;
-  a.bt_width = bt_width;
-  a.lens = lens;
-  a.order = row_order;
-  a.n = n;
-  a.H = num_heads;
-  a.KVH = num_kv_heads;
-  a.D = head_size;
-  a.BS = block_size;
-  a.scale = scale;
-  a.kv_dtype = kv_dtype;
-  a.out = out;
-  a.out_ss = out_stride_seq;
-  a.out_sh = out_stride_head;
-  a.out_dtype = out_dtype;
-  a.lse = lse;
-  a.lse_sh = lse_stride_head;
-  a.workspace = workspace;
-  a.workspace_bytes = workspace_bytes;
-  return launch_decode(a, sp, static_cast<hipStream_t>(stream));
+  a.tier[0] = KvTier{k_cache, v_cache, kv_stride_block, kv_stride_head, kv_stride_token,
+                     num_blocks, block_table, bt_stride, bt_width, lens};
+  a.ntiers = 1;
+  return run_decode(a, "decode", q, q_stride_seq, q_stride_head, row_order, n, num_heads,
+                    num_kv_heads, head_size, block_size, scale, kv_dtype, out, out_stride_seq,
+                    out_stride_head, out_dtype, lse, lse_stride_head, workspace,
+                    workspace_bytes, stream);
+}
+
+int fd_split_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+                    const fd_kv_tier* hbm, const fd_kv_tier* host, const int32_t* row_order,
+                    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                    int32_t block_size, float scale, int32_t kv_dtype, void* out,
+                    int64_t out_stride_seq, int64_t out_stride_head, int32_t out_dtype,
+                    float* lse, int64_t lse_stride_head, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  if (hbm == nullptr || host == nullptr)
+    return set_error(FD_ERR_INVALID, "split_decode: NULL tier descriptor");
+  DecodeArgs a{};
+  const fd_kv_tier* tiers[2] = {hbm, host};
+  for (int t = 0; t < 2; ++t) {
+    const fd_kv_tier& d = *tiers[t];
+    a.tier[t] = KvTier{d.k_cache, d.v_cache, d.stride_block, d.stride_head, d.stride_token,
+                       d.num_blocks, d.block_table, d.bt_stride, d.bt_width, d.lens};
+  }
+  a.ntiers = 2;
+  return run_decode(a, "split_decode", q, q_stride_seq, q_stride_head, row_order, n, num_heads,
+                    num_kv_heads, head_size, block_size, scale, kv_dtype, out, out_stride_seq,
+                    out_stride_head, out_dtype, lse, lse_stride_head, workspace,
+                    workspace_bytes, stream);
 }
 
 int fd_merge_attn_states(void* out, int64_t out_stride_seq, int64_t out_stride_head,

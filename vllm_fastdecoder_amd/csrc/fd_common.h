@@ -123,14 +123,6 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
-// Max over aligned groups of 16 lanes (one DPP row); every lane receives it.
-__device__ __forceinline__ float row_max16(float x) {
-  x = fmaxf(x, dpp<kDppQuadXor1>(x));
-  x = fmaxf(x, dpp<kDppQuadXor2>(x));
-  x = fmaxf(x, dpp<kDppRowHalfMirror>(x));
-  return fmaxf(x, dpp<kDppRowMirror>(x));
-}
-
 __device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
   return __shfl_xor(x, mask, kWave);
 }
@@ -156,17 +148,25 @@ __device__ __forceinline__ float qnan() { return __builtin_nanf(""); }
 // ---------------------------------------------------------------- launchers
 // Implemented in decode_partial.hip / merge.hip / cache_write.hip; the C ABI
 // in capi.hip validates arguments and then calls these.
-struct DecodeArgs {
-  const void* q;
-  int64_t q_ss, q_sh;
+// One KV tier of a decode call: its own cache, strides, table and lengths.
+struct KvTier {
   const void* k;
   const void* v;
-  int64_t kv_sb, kv_sh, kv_st;
+  int64_t sb, sh, st;  // element strides: block, head, token
   int64_t num_blocks;
   const int32_t* bt;
   int64_t bt_stride;
   int32_t bt_width;
   const int32_t* lens;
+};
+
+// A decode call over one tier (a partial) or two (the fused split path: each
+// row's tier-0 blocks, then its tier-1 blocks, as one list).
+struct DecodeArgs {
+  const void* q;
+  int64_t q_ss, q_sh;
+  KvTier tier[2];
+  int32_t ntiers;
   const int32_t* order;  // optional sequence processing order (may be NULL)
   int32_t n, H, KVH, D, BS;
   float scale;

@@ -154,6 +154,107 @@ def paged_decode_partial(
     )
 
 
+def _tier(k_cache, v_cache, strides, num_blocks, block_table, lens, n, dev, what):
+    """fd_kv_tier for one tier (plus the index tensors it points at, which the
+    caller keeps alive until the launch is enqueued)."""
+    _require(block_table.dtype == torch.int32 and lens.dtype == torch.int32,
+             f"{what}: block_table and lens must be int32")
+    _require(block_table.dim() == 2 and block_table.shape[0] == n and lens.shape == (n,),
+             f"{what}: block_table must be [n, W] and lens [n]")
+    _require(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape,
+             f"{what}: k and v caches must share shape and strides")
+    _require(k_cache.stride(-1) == 1, f"{what}: caches must be contiguous in head_size")
+    bt = _on_device(block_table, dev)
+    _require(bt.stride(1) == 1 or bt.shape[1] <= 1, f"{what}: block_table rows must be contiguous")
+    ln = _on_device(lens, dev).contiguous()
+    desc = _lib.FdKvTier(
+        device_ptr(k_cache), device_ptr(v_cache), strides[0], strides[1], strides[2], num_blocks,
+        bt.data_ptr(), bt.stride(0), bt.shape[1], ln.data_ptr(),
+    )
+    return desc, (bt, ln)
+
+
+def split_decode(
+    q: torch.Tensor,
+    hbm_key_cache: torch.Tensor,
+    hbm_value_cache: torch.Tensor,
+    hbm_block_table: torch.Tensor,
+    hbm_lens: torch.Tensor,
+    host_k_cache: torch.Tensor,
+    host_v_cache: torch.Tensor,
+    host_block_table: torch.Tensor,
+    host_lens: torch.Tensor,
+    softmax_scale: float,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+    row_order: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused split decode: attention over each row's HBM-tier and host-tier
+    blocks in one launch, i.e. the GPU-tier partial, the host-tier partial and
+    their merge of fastdecode/backend.py:293-356 in one call (the result of
+    paged_decode + decode_attn + merge_attn_states, up to fp32 summation
+    order).
+
+    hbm_key_cache / hbm_value_cache [B, BS, KVH, D]: vLLM's cache halves;
+    host_k_cache / host_v_cache [C, KVH, BS, D]: the pinned host tier;
+    *_block_table int32 [n, W] tier-relative ids in sequence order and
+    *_lens int32 [n] tier token counts (the planner's s_gpu_bt / s_gpu_lens
+    and s_cpu_bt / s_cpu_lens; 0 allowed in either). Returns out [n, H, D]
+    (q's dtype unless `out` is given) and lse [H, n] float32.
+    """
+    _require(q.is_cuda and q.dim() == 3 and q.stride(2) == 1, "q must be [n, H, D] on the GPU")
+    n, H, D = q.shape
+    _require(hbm_key_cache.dim() == 4 and host_k_cache.dim() == 4, "caches must be 4-d")
+    B, BS, KVH, Dk = hbm_key_cache.shape
+    C, KVH2, BS2, Dh = host_k_cache.shape
+    _require(Dk == D and Dh == D and KVH2 == KVH and BS2 == BS,
+             "the tiers' head size, kv heads and block size must agree with q")
+    _require(H % KVH == 0, "num_heads must be a multiple of num_kv_heads")
+    kv_dt = _dtype_code(q, "q")
+    for t in (hbm_key_cache, hbm_value_cache, host_k_cache, host_v_cache):
+        _require(t.dtype == q.dtype, "q and the caches must share a dtype")
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty(H, n, dtype=torch.float32, device=q.device)
+    _require(out.is_cuda and out.shape == q.shape and out.stride(2) == 1,
+             "out must be [n, H, D] on the GPU")
+    _require(out.dtype == q.dtype or out.dtype == torch.float32, "out must be q's dtype or float32")
+    _require(lse.dtype == torch.float32 and tuple(lse.shape) == (H, n) and (n == 0 or lse.stride(1) == 1),
+             "lse must be float32 [H, n] with contiguous rows")
+    if n == 0:
+        return out, lse
+    dev = q.device
+    hbm, keep_a = _tier(hbm_key_cache, hbm_value_cache,
+                        (hbm_key_cache.stride(0), hbm_key_cache.stride(2), hbm_key_cache.stride(1)),
+                        B, hbm_block_table, hbm_lens, n, dev, "hbm tier")
+    host, keep_b = _tier(host_k_cache, host_v_cache,
+                         (host_k_cache.stride(0), host_k_cache.stride(1), host_k_cache.stride(2)),
+                         C, host_block_table, host_lens, n, dev, "host tier")
+    need = workspace_bytes(n, H, KVH, D, BS, hbm.bt_width + host.bt_width)
+    ws = WORKSPACE.get(dev, need)
+    order_ptr = None
+    if row_order is not None:
+        _require(row_order.dtype == torch.int32 and row_order.shape == (n,),
+                 "row_order must be int32 [n]")
+        row_order = _on_device(row_order, dev).contiguous()
+        order_ptr = row_order.data_ptr()
+    lib = _lib.load_lib()
+    _lib.check(
+        lib.fd_split_decode(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            ctypes.byref(hbm), ctypes.byref(host), order_ptr,
+            n, H, KVH, D, BS, float(softmax_scale), kv_dt,
+            out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
+            lse.data_ptr(), lse.stride(0),
+            ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+            _stream_for(q),
+        )
+    )
+    del keep_a, keep_b  # the launch is enqueued; later reuse is stream-ordered
+    return out, lse
+
+
 def longest_first(lens: torch.Tensor) -> torch.Tensor:
     """int32 permutation of the rows by decreasing length, computed on the
     host (the planner already holds the lengths there)."""

@@ -233,6 +233,7 @@ class DevicePlan:
     # scheduling order of the S rows for each tier's partial: longest first
     s_gpu_order: torch.Tensor | None = None  # [nS] int32
     s_cpu_order: torch.Tensor | None = None  # [nS] int32
+    s_order: torch.Tensor | None = None  # [nS] int32, by both tiers' tokens (fused path)
 
 
 def longest_first(lens: torch.Tensor) -> torch.Tensor:
@@ -268,4 +269,5 @@ def to_device(hp: HostPlan, block_table_dev: torch.Tensor, device) -> DevicePlan
         host_slot_mapping=d(hp.host_slot_mapping) if hp.host_slot_mapping is not None else None,
         s_gpu_order=d(longest_first(hp.s_gpu_lens)),
         s_cpu_order=d(longest_first(hp.s_cpu_lens)),
+        s_order=d(longest_first(hp.s_gpu_lens + hp.s_cpu_lens)),
     )
