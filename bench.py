@@ -85,6 +85,21 @@ def algorithmic_bytes(lens, n, H, KVH, D, BS, elt, out_elt):
     return kv + n * H * D * elt + n * H * D * out_elt + 4 * n * H + 4 * int(nb.sum()) + 4 * n, kv
 
 
+# The decode kernels' sources, hashed together to tie a committed counter
+# profile to the exact code it measured.
+KERNEL_SOURCES = ("fd_common.h", "decode_tiled.h", "decode_valu.hip", "decode_mfma.hip",
+                  "decode_partial.hip")
+
+
+def kernel_source_sha() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        h.update((ROOT / "vllm_fastdecoder_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()[:16]
+
+
 def time_gpu(fn, steps, warmup, stream):
     import torch
 
@@ -303,10 +318,7 @@ def main() -> int:
     traffic = None
     prof = ROOT / "profiles" / f"traffic_{w.name}_{args.layout}.json"
     if prof.exists():
-        import hashlib
-
-        src = ROOT / "vllm_fastdecoder_amd" / "csrc" / "decode_partial.hip"
-        sha = hashlib.sha256(src.read_bytes()).hexdigest()[:16]
+        sha = kernel_source_sha()
         try:
             rec = json.loads(prof.read_text())
             if rec.get("source_sha256_16") == sha:
