@@ -174,6 +174,46 @@ def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
     }
 
 
+def time_planners(w, bt_g, len_g, bt_c, len_c, G, C, dev, iters=50):
+    """Per-step planning of the split run's decode step (one new token per
+    row): the reference's host planner (a device-to-host copy of the table
+    and slots, host compaction, upload; backend.build_split_plan) against
+    the device tier split (backend.build_device_step, no copy back). Wall
+    time per step, the GPU otherwise idle."""
+    import torch
+
+    from vllm_fastdecoder_amd import backend, state
+
+    n, W = bt_g.shape
+    nbg = (len_g + w.BS - 1) // w.BS
+    nbc = (len_c + w.BS - 1) // w.BS
+    uni = torch.zeros(n, 2 * W, dtype=torch.int32)
+    slots = torch.zeros(n, dtype=torch.int64)
+    for i in range(n):
+        a, b = int(nbg[i]), int(nbc[i])
+        uni[i, :a] = bt_g[i, :a]
+        uni[i, a:a + b] = bt_c[i, :b] + G
+        L = int(len_g[i] + len_c[i])
+        last = int(uni[i, (L - 1) // w.BS])
+        slots[i] = last * w.BS + (L - 1) % w.BS
+    seq = (len_g + len_c).to(torch.int32)
+    qsl = torch.arange(n + 1, dtype=torch.int32)
+    store = state.HostKVStore(G, C, w.BS, w.KVH, w.D, w.dtype)
+    uni_d, slots_d = uni.to(dev), slots.to(dev)
+    out = {}
+    for name, fn in (("host_ms", backend.build_split_plan), ("device_ms", backend.build_device_step)):
+        for _ in range(5):
+            fn(qsl, seq, uni_d, slots_d, n, store, dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn(qsl, seq, uni_d, slots_d, n, store, dev)
+        torch.cuda.synchronize()
+        out[name] = round((time.perf_counter() - t0) / iters * 1e3, 3)
+    out["note"] = "per-step planning, wall time; host = device-to-host copy + host compaction"
+    return out
+
+
 def split_run(w, lens, bt, q, steps, warmup, stream):
     """60% of each row's blocks (the last ones) in pinned host memory, the rest
     in HBM: HBM partial + host partial (zero-copy) + LSE merge, and the same
@@ -252,6 +292,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     t_merge = time_gpu(merge, steps, warmup, stream)
     t_step = time_gpu(step, host_steps, 1, stream)
     t_fused = time_gpu(fused, host_steps, 1, stream)
+    planner = time_planners(w, bt_g, len_g, bt_c, len_c, G, C, dev)
     b_hbm, kv_hbm = algorithmic_bytes(len_g, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     b_host, kv_host = algorithmic_bytes(len_c, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     del kv, hk, hv
@@ -266,6 +307,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "step_tokens_per_s": round(w.n / (t_step / 1e3 * LAYERS), 1),
         "fused_step_ms": round(t_fused, 3),
         "fused_step_tokens_per_s": round(w.n / (t_fused / 1e3 * LAYERS), 1),
+        "planner": planner,
         "note": "host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not `value`",
     }
 

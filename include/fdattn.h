@@ -174,6 +174,43 @@ int fd_split_decode(
     void* stream);
 
 /* ------------------------------------------------------------------------
+ * Device-side tier split of a decode step.
+ *
+ * The part of the reference's per-step planner build_host_plan
+ * (fastdecode/plan.py:103-199, run on the host after a device-to-host copy of
+ * the block table, fastdecode/backend.py:140-178) that a decode step needs,
+ * computed on the GPU so the step needs no device-to-host copy. For every row
+ * r < n_rows with seq_lens[r] tokens in blocks block_table[r, 0 .. nb):
+ *   gpu_block_table[r, :] = its ids < num_gpu_blocks, in order, then zeros;
+ *   cpu_block_table[r, :] = its ids >= num_gpu_blocks minus num_gpu_blocks,
+ *                           in order, then zeros  (plan.py:82-100);
+ *   gpu_lens[r], cpu_lens[r] = tokens held by each tier's blocks, the row's
+ *                           last block holding L - (nb-1)*block_size
+ *                           (plan.py:165-170).
+ * For every token t < n_tokens (plan.py:150-152):
+ *   gpu_slot_mapping[t]  = -1 for a host slot (>= num_gpu_blocks*block_size),
+ *                          else slot_mapping[t];
+ *   host_slot_mapping[t] = slot - num_gpu_blocks*block_size for a host slot,
+ *                          else -1.
+ * A host id past num_gpu_blocks + num_cpu_blocks, or a length needing more
+ * than bt_width blocks, adds to *error_count (may be NULL) -- the
+ * planner's RuntimeError, reported asynchronously; the row's lengths then
+ * make the decode kernels write NaN for it. The outputs have width
+ * out_width >= bt_width and row stride out_stride. Feeding both tables to
+ * fd_split_decode (HBM tier, host tier) decodes every row, P and S alike.
+ * ------------------------------------------------------------------------ */
+int fd_plan_tiers(
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* seq_lens, int32_t n_rows,
+    int32_t num_gpu_blocks, int64_t num_cpu_blocks, int32_t block_size,
+    int32_t* gpu_block_table, int32_t* cpu_block_table,
+    int64_t out_stride, int32_t out_width,
+    int32_t* gpu_lens, int32_t* cpu_lens,
+    const int64_t* slot_mapping, int32_t n_tokens,
+    int64_t* gpu_slot_mapping, int64_t* host_slot_mapping,
+    int32_t* error_count, void* stream);
+
+/* ------------------------------------------------------------------------
  * Log-sum-exp merge of two partials.
  *
  * Replaces vLLM's merge_attn_states(out, o_a, lse_a, o_b, lse_b) called at

@@ -67,7 +67,8 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                    H: int = 32, KVH: int = 32, D: int = 128, BS: int = 16,
                    dtype: torch.dtype = torch.float16, arrivals: float = 4.0,
                    prompt: tuple[int, int] = (64, 512), output: tuple[int, int] = (32, 512),
-                   tol: float = 3e-3, oracle_every: int = 25, fused: bool = True) -> dict:
+                   tol: float = 3e-3, oracle_every: int = 25, fused: bool = True,
+                   planner: str = "host") -> dict:
     dev = device or torch.device("cuda", 0)
     rng = random.Random(seed)
     nrng = np.random.default_rng(seed)
@@ -111,7 +112,9 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
 
     running = []
     stats = {"failures": [], "split_steps": 0, "decode_rows": 0, "split_rows": 0,
-             "host_tokens": 0, "max_err_vs_mono": 0.0, "max_err_vs_f64": 0.0, "dropped": 0}
+             "host_tokens": 0, "max_err_vs_mono": 0.0, "max_err_vs_f64": 0.0, "dropped": 0,
+             "device_planned_steps": 0}
+    plan_errors = torch.zeros(1, dtype=torch.int32, device=dev)
     try:
         for step in range(steps):
             rows = []
@@ -166,8 +169,15 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
 
             # ---- split path
             out_split = torch.full((Tp, H, D), float("nan"), dtype=dtype, device=dev)
-            dp = backend.build_split_plan(qsl, seq, bt_d, slots_d, R, store, dev)
-            if dp is None:
+            ds = (backend.build_device_step(qsl, seq, bt_d, slots_d, R, store, dev)
+                  if planner == "device" else None)
+            dp = backend.build_split_plan(qsl, seq, bt_d, slots_d, R, store, dev) \
+                if ds is None else None
+            if ds is not None:
+                stats["device_planned_steps"] += 1
+                impl._forward_device(layer, q, k, v, kv_cache, ds, out_split)
+                plan_errors += ds.errors
+            elif dp is None:
                 ops.reshape_and_cache(k, v, kv_cache.transpose(1, 2)[..., :D],
                                       kv_cache.transpose(1, 2)[..., D:], slots_d)
                 dec = [i for i in range(R) if qlens[i] == 1]
@@ -236,6 +246,8 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                     running.remove(r)
                     release(r["blocks"])
         torch.cuda.synchronize()
+        if int(plan_errors.item()):
+            stats["failures"].append(f"device planner counted {int(plan_errors.item())} errors")
     finally:
         state.STORE = prev_store
         backend.OPS = prev_ops

@@ -197,19 +197,25 @@ def test_hipops_fa_rejects_prefill_forms(gpu):
                           softmax_scale=0.1, causal=True)
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_continuous_batching_simulation(gpu, fused):
+@pytest.mark.parametrize("fused,planner", [(True, "host"), (False, "host"), (True, "device")])
+def test_continuous_batching_simulation(gpu, fused, planner):
     """The config of the reference's GPU self-test at vicuna-7b head shapes:
     300 decode steps, G=256 HBM blocks, C=2048 host blocks, Poisson(4)
     arrivals, prompts U[64,512], outputs U[32,512], GPU-first allocation with
     block reuse; every step checked against monolithic attention over one
     G+C pool written with the same KV, and every slot written bit-exact. S
-    rows through the fused launch and through two partials + merge."""
+    rows through the fused launch and through two partials + merge, with the
+    step planned on the host (one device-to-host copy per step, as in the
+    reference) or on the GPU (none)."""
     from tests.simulate import run_simulation
 
-    stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused)
+    stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused, planner=planner)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
-    assert stats["split_steps"] > 100 and stats["decode_rows"] > 1000
+    assert stats["decode_rows"] > 1000
+    if planner == "device":
+        assert stats["device_planned_steps"] > 250
+    else:
+        assert stats["split_steps"] > 100
     assert stats["max_err_vs_mono"] <= 3e-3
     assert stats["max_err_vs_f64"] <= 3e-3

@@ -77,6 +77,20 @@ SIGNATURES: dict[str, tuple] = {
             c_void_p,                              # stream
         ],
     ),
+    "fd_plan_tiers": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int32,            # block_table, bt_stride, bt_width
+            c_void_p, c_int32,                     # seq_lens, n_rows
+            c_int32, c_int64, c_int32,             # G, C, block_size
+            c_void_p, c_void_p, c_int64, c_int32,  # gpu/cpu tables, out stride, width
+            c_void_p, c_void_p,                    # gpu_lens, cpu_lens
+            c_void_p, c_int32,                     # slot_mapping, n_tokens
+            c_void_p, c_void_p,                    # gpu / host slot mappings
+            c_void_p,                              # error_count
+            c_void_p,                              # stream
+        ],
+    ),
     "fd_merge_attn_states": (
         c_int,
         [

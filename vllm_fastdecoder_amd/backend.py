@@ -18,6 +18,9 @@ vLLM's base classes:
     no longer computed on the host: its KV rows are written into the pinned
     tier by the GPU and its partial is read zero-copy by the GPU, so there is
     no staging copy and no host wait.
+  * `build_device_step` / `SplitDecodeImpl._forward_device` -- this build's
+    addition: the same step planned on the GPU (fd_plan_tiers), with no
+    device-to-host copy, for steps whose prefill rows (if any) are fresh.
 """
 
 from __future__ import annotations
@@ -27,7 +30,7 @@ from dataclasses import dataclass
 import torch
 
 from . import ops, state
-from .plan import DevicePlan, build_host_plan, to_device
+from .plan import DevicePlan, build_host_plan, longest_first, to_device
 
 
 class HipOps:
@@ -98,6 +101,73 @@ def build_split_plan(query_start_loc_cpu: torch.Tensor, seq_lens_cpu: torch.Tens
     if hp is None:
         return None
     return to_device(hp, bt_dev[:, :width], device)
+
+
+@dataclass
+class DeviceStep:
+    """A step planned on the GPU: every row's per-tier tables, lengths and the
+    split slot mapping (device tensors), plus what the host already knows
+    from the step's CPU metadata: which tokens are decode rows and which
+    belong to fresh prefills."""
+
+    gpu_bt: torch.Tensor  # [R, W] int32
+    cpu_bt: torch.Tensor  # [R, W] int32
+    gpu_lens: torch.Tensor  # [R] int32
+    cpu_lens: torch.Tensor  # [R] int32
+    gpu_slots: torch.Tensor  # [T] int64
+    host_slots: torch.Tensor  # [T] int64
+    dec_rows: torch.Tensor  # [nD] int64: decode rows (one query token)
+    dec_tok: torch.Tensor  # [nD] int64: their query tokens
+    dec_order: torch.Tensor  # [nD] int32: longest first
+    n_dec: int
+    f_tok: torch.Tensor  # [nF_tok] int64: tokens of fresh prefills
+    f_cu: torch.Tensor  # [nF + 1] int32
+    f_max: int
+    n_f_tok: int
+    errors: torch.Tensor  # [1] int32: host ids past the tier, lengths past the table
+
+
+def build_device_step(query_start_loc_cpu: torch.Tensor, seq_lens_cpu: torch.Tensor,
+                      block_table: torch.Tensor, slot_mapping: torch.Tensor, num_reqs: int,
+                      store: state.HostKVStore | None, device) -> DeviceStep | None:
+    """Plans a step on the GPU (fd_plan_tiers): no device-to-host copy. None
+    when no host tier is set up, or when a prefill row extends prior context
+    (whether it touches the host tier is only known on the device; such
+    steps take build_split_plan, where the reference's rule applies,
+    plan.py:142-149)."""
+    if store is None or num_reqs == 0:
+        return None
+    qsl = query_start_loc_cpu[: num_reqs + 1].to(torch.int64)
+    seq = seq_lens_cpu[:num_reqs].to(torch.int64)
+    qlen = qsl[1:] - qsl[:-1]
+    ctx = seq - qlen
+    if bool(((qlen > 1) & (ctx > 0)).any()):
+        return None
+    def d(t: torch.Tensor) -> torch.Tensor:
+        # host metadata to the device through pinned memory: no host wait
+        return t.pin_memory().to(device, non_blocking=True)
+
+    n_tok = int(qsl[-1])
+    bs = store.block_size
+    width = max(1, min(int((int(seq.max()) + bs - 1) // bs), block_table.shape[1]))
+    errors = torch.zeros(1, dtype=torch.int32, device=device)
+    gpu_bt, cpu_bt, gpu_lens, cpu_lens, gpu_slots, host_slots = ops.plan_tiers(
+        block_table[:num_reqs, :width], d(seq.to(torch.int32)), slot_mapping[:n_tok],
+        store.num_gpu_blocks, store.num_cpu_blocks, bs, error_count=errors)
+    dec = torch.nonzero(qlen == 1).flatten()
+    fre = torch.nonzero(qlen > 1).flatten()
+    f_q = qlen[fre]
+    f_tok = torch.cat([torch.arange(int(qsl[r]), int(qsl[r + 1])) for r in fre.tolist()]) \
+        if fre.numel() else torch.zeros(0, dtype=torch.int64)
+    f_cu = torch.zeros(fre.numel() + 1, dtype=torch.int32)
+    f_cu[1:] = torch.cumsum(f_q, 0).to(torch.int32)
+    return DeviceStep(
+        gpu_bt=gpu_bt, cpu_bt=cpu_bt, gpu_lens=gpu_lens, cpu_lens=cpu_lens,
+        gpu_slots=gpu_slots, host_slots=host_slots,
+        dec_rows=d(dec), dec_tok=d(qsl[dec]), dec_order=d(longest_first(seq[dec])),
+        n_dec=int(dec.numel()), f_tok=d(f_tok), f_cu=d(f_cu),
+        f_max=int(f_q.max()) if f_q.numel() else 0, n_f_tok=int(f_tok.numel()), errors=errors,
+    )
 
 
 @dataclass
@@ -196,4 +266,49 @@ class SplitDecodeImpl:
                 merged = torch.empty_like(qs)
                 OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
             output.index_copy_(0, dp.s_tok, merged)
+        return output
+
+    def _forward_device(self, layer, query, key, value, kv_cache, ds: DeviceStep, output):
+        """The step of _forward_split planned on the GPU (build_device_step):
+        KV writes into both tiers from the split slot mapping, every decode row
+        (all-HBM and split alike) through one fused two-tier launch, fresh
+        prefills through the prefill form of OPS.fa. No device-to-host copy."""
+        store = state.STORE
+        assert store is not None, "no host KV tier (state.ensure_store)"
+        k_host = store.k[layer.layer_name]
+        v_host = store.v[layer.layer_name]
+        D = self.head_size
+        key_cache, value_cache = kv_cache.transpose(1, 2).split(D, dim=-1)
+
+        # 1) KV writes: both tiers by slot, slots of the other tier are -1
+        if self.kv_sharing_target_layer_name is None:
+            OPS.reshape_and_cache(key, value, key_cache, value_cache, ds.gpu_slots,
+                                  self.kv_cache_dtype, getattr(layer, "_k_scale", None),
+                                  getattr(layer, "_v_scale", None))
+            ops.reshape_and_cache(key, value, k_host.transpose(1, 2), v_host.transpose(1, 2),
+                                  ds.host_slots)
+
+        # 2) decode rows: both tiers in one launch (a row without host tokens
+        #    is plain paged attention over its HBM blocks)
+        if ds.n_dec:
+            q = query.index_select(0, ds.dec_tok)
+            out, _ = OPS.split_decode(q, key_cache, value_cache,
+                                      ds.gpu_bt.index_select(0, ds.dec_rows),
+                                      ds.gpu_lens.index_select(0, ds.dec_rows), k_host, v_host,
+                                      ds.cpu_bt.index_select(0, ds.dec_rows),
+                                      ds.cpu_lens.index_select(0, ds.dec_rows),
+                                      float(self.scale), row_order=ds.dec_order)
+            output.index_copy_(0, ds.dec_tok, out)
+
+        # 3) fresh prefills attend only this step's q/k/v (backend.py:331-340)
+        if ds.n_f_tok:
+            q_f = query.index_select(0, ds.f_tok)
+            k_f = key.index_select(0, ds.f_tok)
+            v_f = value.index_select(0, ds.f_tok)
+            o_f = OPS.fa(
+                q=q_f, k=k_f, v=v_f, cu_seqlens_q=ds.f_cu, cu_seqlens_k=ds.f_cu,
+                max_seqlen_q=ds.f_max, max_seqlen_k=ds.f_max, softmax_scale=self.scale,
+                causal=True, softcap=self.logits_soft_cap,
+            )
+            output.index_copy_(0, ds.f_tok, o_f)
         return output

@@ -182,6 +182,50 @@ int fd_split_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,
                     workspace_bytes, stream);
 }
 
+int fd_plan_tiers(const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+                  const int32_t* seq_lens, int32_t n_rows, int32_t num_gpu_blocks,
+                  int64_t num_cpu_blocks, int32_t block_size, int32_t* gpu_block_table,
+                  int32_t* cpu_block_table, int64_t out_stride, int32_t out_width,
+                  int32_t* gpu_lens, int32_t* cpu_lens, const int64_t* slot_mapping,
+                  int32_t n_tokens, int64_t* gpu_slot_mapping, int64_t* host_slot_mapping,
+                  int32_t* error_count, void* stream) {
+  if (n_rows < 0 || n_tokens < 0 || bt_width < 0 || num_gpu_blocks < 0 || num_cpu_blocks < 0 ||
+      block_size <= 0)
+    return set_error(FD_ERR_INVALID, "plan_tiers: bad sizes");
+  if (n_rows > 0) {
+    if (!block_table || !seq_lens || !gpu_block_table || !cpu_block_table || !gpu_lens ||
+        !cpu_lens)
+      return set_error(FD_ERR_INVALID, "plan_tiers: NULL row pointer");
+    if (bt_width > 0 && bt_stride < bt_width)
+      return set_error(FD_ERR_INVALID, "plan_tiers: bt_stride < bt_width");
+    if (out_width < bt_width || out_stride < out_width)
+      return set_error(FD_ERR_INVALID, "plan_tiers: output tables narrower than the input");
+  }
+  if (n_tokens > 0 && (!slot_mapping || !gpu_slot_mapping || !host_slot_mapping))
+    return set_error(FD_ERR_INVALID, "plan_tiers: NULL slot pointer");
+  PlanTiersArgs a{};
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.seq_lens = seq_lens;
+  a.n_rows = n_rows;
+  a.G = num_gpu_blocks;
+  a.C = num_cpu_blocks;
+  a.BS = block_size;
+  a.gpu_bt = gpu_block_table;
+  a.cpu_bt = cpu_block_table;
+  a.out_stride = out_stride;
+  a.out_width = out_width;
+  a.gpu_lens = gpu_lens;
+  a.cpu_lens = cpu_lens;
+  a.slots = slot_mapping;
+  a.n_tokens = n_tokens;
+  a.gpu_slots = gpu_slot_mapping;
+  a.host_slots = host_slot_mapping;
+  a.error_count = error_count;
+  return launch_plan_tiers(a, static_cast<hipStream_t>(stream));
+}
+
 int fd_merge_attn_states(void* out, int64_t out_stride_seq, int64_t out_stride_head,
                          int32_t out_dtype, const void* o_a, int64_t a_stride_seq,
                          int64_t a_stride_head, int32_t a_dtype, const float* lse_a,

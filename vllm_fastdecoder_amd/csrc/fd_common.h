@@ -233,4 +233,28 @@ int launch_cache_write(const CacheWriteArgs& a, hipStream_t s);
 
 int launch_stream_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 
+// Device-side tier split of a decode step (plan_tiers.hip).
+struct PlanTiersArgs {
+  const int32_t* bt;
+  int64_t bt_stride;
+  int32_t bt_width;
+  const int32_t* seq_lens;
+  int32_t n_rows;
+  int32_t G;  // HBM blocks: ids < G are in HBM
+  int64_t C;  // host blocks: ids in [G, G + C)
+  int32_t BS;
+  int32_t* gpu_bt;
+  int32_t* cpu_bt;
+  int64_t out_stride;
+  int32_t out_width;
+  int32_t* gpu_lens;
+  int32_t* cpu_lens;
+  const int64_t* slots;
+  int32_t n_tokens;
+  int64_t* gpu_slots;
+  int64_t* host_slots;
+  int32_t* error_count;
+};
+int launch_plan_tiers(const PlanTiersArgs& a, hipStream_t s);
+
 }  // namespace fd

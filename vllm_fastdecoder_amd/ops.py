@@ -255,6 +255,54 @@ def split_decode(
     return out, lse
 
 
+def plan_tiers(block_table: torch.Tensor, seq_lens: torch.Tensor, slot_mapping: torch.Tensor,
+               num_gpu_blocks: int, num_cpu_blocks: int, block_size: int,
+               error_count: torch.Tensor | None = None):
+    """Device-side tier split of a step (fd_plan_tiers): the per-row, per-tier
+    block compaction and token counts and the slot split of
+    fastdecode/plan.py:82-100,150-152,165-170, computed on the GPU.
+
+    block_table int32 [R, W] on the GPU; seq_lens int32 [R] (a host tensor is
+    uploaded, never read back); slot_mapping int64 [T] on the GPU;
+    error_count optional int32 [1] GPU counter of host ids past the host tier
+    and of lengths past the table. Returns (gpu_bt [R, W], cpu_bt [R, W],
+    gpu_lens [R], cpu_lens [R], gpu_slots [T], host_slots [T])."""
+    _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2,
+             "block_table must be int32 [R, W] on the GPU")
+    R, W = block_table.shape
+    dev = block_table.device
+    _require(R == 0 or W <= 1 or block_table.stride(1) == 1, "block_table rows must be contiguous")
+    _require(seq_lens.dtype == torch.int32 and seq_lens.shape == (R,), "seq_lens must be int32 [R]")
+    _require(slot_mapping.dtype == torch.int64 and slot_mapping.dim() == 1,
+             "slot_mapping must be int64 [T]")
+    T = slot_mapping.shape[0]
+    ln = _on_device(seq_lens, dev).contiguous()
+    sm = _on_device(slot_mapping, dev).contiguous()
+    gpu_bt = torch.empty(R, W, dtype=torch.int32, device=dev)
+    cpu_bt = torch.empty(R, W, dtype=torch.int32, device=dev)
+    gpu_lens = torch.empty(R, dtype=torch.int32, device=dev)
+    cpu_lens = torch.empty(R, dtype=torch.int32, device=dev)
+    gpu_slots = torch.empty(T, dtype=torch.int64, device=dev)
+    host_slots = torch.empty(T, dtype=torch.int64, device=dev)
+    err_ptr = None
+    if error_count is not None:
+        _require(error_count.is_cuda and error_count.dtype == torch.int32, "error_count: int32 GPU")
+        err_ptr = error_count.data_ptr()
+    _lib.check(
+        _lib.load_lib().fd_plan_tiers(
+            block_table.data_ptr(), block_table.stride(0) if R else W, W,
+            ln.data_ptr(), R,
+            int(num_gpu_blocks), int(num_cpu_blocks), int(block_size),
+            gpu_bt.data_ptr(), cpu_bt.data_ptr(), W, W,
+            gpu_lens.data_ptr(), cpu_lens.data_ptr(),
+            sm.data_ptr(), T,
+            gpu_slots.data_ptr(), host_slots.data_ptr(),
+            err_ptr, _stream_for(block_table),
+        )
+    )
+    return gpu_bt, cpu_bt, gpu_lens, cpu_lens, gpu_slots, host_slots
+
+
 def longest_first(lens: torch.Tensor) -> torch.Tensor:
     """int32 permutation of the rows by decreasing length, computed on the
     host (the planner already holds the lengths there)."""
