@@ -214,6 +214,12 @@ def time_planners(w, bt_g, len_g, bt_c, len_c, G, C, dev, iters=50):
     return out
 
 
+def threads_used():
+    from vllm_fastdecoder_amd import _lib
+
+    return int(_lib.load_lib().fd_host_decode_threads())
+
+
 def split_run(w, lens, bt, q, steps, warmup, stream):
     """60% of each row's blocks (the last ones) in pinned host memory, the rest
     in HBM: HBM partial + host partial (zero-copy) + LSE merge, and the same
@@ -286,7 +292,30 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         ops.split_decode(q, kc_g, vc_g, bt_g_d, len_g_d, hk, hv, bt_c_d, len_c_d, w.scale,
                          out=f_out, lse=f_lse, row_order=ord_all)
 
+    # hybrid: each row's trailing host blocks reduced by the host cores while
+    # the GPU reads the HBM tier and the leading host blocks over the link
+    q_host = q.cpu()
+    o_h = torch.empty(w.n, w.H, w.D, dtype=torch.float32)
+    l_h = torch.empty(w.H, w.n, dtype=torch.float32)
+    h_out = torch.empty_like(o_g)
+    h_lse = torch.empty_like(l_g)
+
+    def host_cores():
+        ops.host_decode_attn(q_host, hk, hv, bt_c, len_c, w.scale, o_h, l_h)
+
+    def hybrid(frac):
+        return lambda: ops.hybrid_split_decode(q, kc_g, vc_g, bt_g_d, len_g, hk, hv, bt_c, len_c,
+                                               w.scale, frac, out=h_out, lse=h_lse)
+
     host_steps = max(2, min(steps, 5))
+    host_cores()
+    t0 = time.perf_counter()
+    for _ in range(host_steps):
+        host_cores()
+    t_cores = (time.perf_counter() - t0) / host_steps * 1e3
+    fracs = (0.5, 0.6, 0.7, 0.8, 0.9)
+    t_hybrid = {f: time_gpu(hybrid(f), host_steps, 1, stream) for f in fracs}
+    f_best = min(t_hybrid, key=t_hybrid.get)
     t_hbm = time_gpu(hbm, steps, warmup, stream)
     t_host = time_gpu(host, host_steps, 1, stream)
     t_merge = time_gpu(merge, steps, warmup, stream)
@@ -295,7 +324,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     planner = time_planners(w, bt_g, len_g, bt_c, len_c, G, C, dev)
     b_hbm, kv_hbm = algorithmic_bytes(len_g, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     b_host, kv_host = algorithmic_bytes(len_c, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
-    del kv, hk, hv
+    del kv, hk, hv, q_host
     return {
         "host_fraction_blocks": 0.6,
         "hbm_partial_ms": round(t_hbm, 4),
@@ -307,8 +336,17 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "step_tokens_per_s": round(w.n / (t_step / 1e3 * LAYERS), 1),
         "fused_step_ms": round(t_fused, 3),
         "fused_step_tokens_per_s": round(w.n / (t_fused / 1e3 * LAYERS), 1),
+        "host_cores_ms": round(t_cores, 3),
+        "host_cores_GBps": round(kv_host / (t_cores / 1e3) / 1e9, 2),
+        "host_cores": threads_used(),
+        "hybrid_step_ms": {str(f): round(t, 3) for f, t in t_hybrid.items()},
+        "hybrid_best_cpu_fraction": f_best,
+        "hybrid_best_step_ms": round(t_hybrid[f_best], 3),
+        "hybrid_best_tokens_per_s": round(w.n / (t_hybrid[f_best] / 1e3 * LAYERS), 1),
         "planner": planner,
-        "note": "host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not `value`",
+        "note": ("host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not "
+                 "`value`; host_cores = fd_host_decode_partial over the whole host tier; "
+                 "hybrid = host cores take the given fraction of each row's host blocks"),
     }
 
 

@@ -290,6 +290,40 @@ int fd_host_free(void* host_ptr);
 int fd_host_device_pointer(void* host_ptr, void** device_ptr);
 
 /* ------------------------------------------------------------------------
+ * Host-core partial decode attention (the co-processing leg of the split step).
+ *
+ * Replaces the reference's host-tier kernel decode_attn
+ * (fastdecode/csrc/cpu_attn.cpp:452-489, body :298-411), called at
+ * fastdecode/backend.py:350-351, with the same arguments and results as
+ * fd_paged_decode_partial -- except that every pointer is a HOST address
+ * (q, caches, table, lengths, out, lse) and the call runs synchronously on
+ * the calling thread plus a persistent pool of num_threads - 1 workers
+ * (0: one per CPU of the process's affinity mask, or FASTDECODE_CPU_THREADS).
+ * Rows with lens <= 0 give out = 0, lse = -inf; a range error makes the row
+ * NaN. Used to give part of each row's host-tier blocks to the host cores
+ * while the GPU reads the rest over the link; the two partials are then
+ * merged with fd_merge_attn_states. Needs AVX2, FMA and F16C
+ * (FD_ERR_UNSUPPORTED otherwise). Calls are serialised per process.
+ * ------------------------------------------------------------------------ */
+int fd_host_decode_partial(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    int32_t num_threads);
+
+/* Worker count fd_host_decode_partial uses when num_threads is 0. No
+ * counterpart in the reference (it uses OpenMP's default team). */
+int fd_host_decode_threads(void);
+
+/* ------------------------------------------------------------------------
  * Measurement helper: streams `bytes` (a multiple of 16) from src to dst with
  * the same 16-byte vector loads the attention kernel uses. Used to calibrate
  * the HBM-traffic counters and the achievable copy bandwidth. No counterpart

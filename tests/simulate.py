@@ -68,7 +68,7 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                    dtype: torch.dtype = torch.float16, arrivals: float = 4.0,
                    prompt: tuple[int, int] = (64, 512), output: tuple[int, int] = (32, 512),
                    tol: float = 3e-3, oracle_every: int = 25, fused: bool = True,
-                   planner: str = "host") -> dict:
+                   planner: str = "host", cpu_fraction: float = 0.0) -> dict:
     dev = device or torch.device("cuda", 0)
     rng = random.Random(seed)
     nrng = np.random.default_rng(seed)
@@ -94,7 +94,7 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
     backend.OPS = _SimOps
     uphys = (torch.randn(G + C, BS, KVH, 2 * D, device=dev) * 10).to(dtype)
     ukc, uvc = uphys[..., :D], uphys[..., D:]
-    impl = backend.SplitDecodeImpl(H, KVH, D, scale, fused_split=fused)
+    impl = backend.SplitDecodeImpl(H, KVH, D, scale, fused_split=fused, cpu_fraction=cpu_fraction)
 
     free_gpu = list(range(1, G))
     free_host = list(range(G, G + C))

@@ -128,13 +128,14 @@ REQS16 = [
 ]
 
 
-@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("mode", ["fused", "two_partials", "hybrid"])
 @pytest.mark.parametrize("case", ["reqs4", "reqs16"])
 @pytest.mark.parametrize("H,KVH", [(4, 4), (8, 2)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH, dtype, fused):
-    """S rows through the fused launch (default) or the reference's two
-    partials + merge; P and F rows as in the reference."""
+def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH, dtype, mode):
+    """S rows through the fused launch (default), the reference's two
+    partials + merge, or the fused launch with 60% of each row's host blocks
+    on the host cores; P and F rows as in the reference."""
     if case == "reqs4":
         reqs, G, C, BS, D = KATS["classification"]["reqs"], 10, 20, 4, 64
     else:
@@ -143,7 +144,8 @@ def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH,
     hp = plan.build_host_plan(sc.qsl, sc.seq, sc.bt, sc.slots, G, C, BS)
     dp = plan.to_device(hp, sc.bt.to(gpu), gpu)
     state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k}, v={"l0": sc.host_v})
-    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, fused_split=fused)
+    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, fused_split=mode != "two_partials",
+                                   cpu_fraction=0.6 if mode == "hybrid" else 0.0)
     layer = SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None)
     output = torch.full_like(sc.query, float("nan"))
     impl._forward_split(layer, sc.query, sc.key, sc.value, sc.kv_cache, dp, output)
@@ -197,8 +199,10 @@ def test_hipops_fa_rejects_prefill_forms(gpu):
                           softmax_scale=0.1, causal=True)
 
 
-@pytest.mark.parametrize("fused,planner", [(True, "host"), (False, "host"), (True, "device")])
-def test_continuous_batching_simulation(gpu, fused, planner):
+@pytest.mark.parametrize("fused,planner,cpu_fraction",
+                         [(True, "host", 0.0), (False, "host", 0.0), (True, "device", 0.0),
+                          (True, "host", 0.6)])
+def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
     """The config of the reference's GPU self-test at vicuna-7b head shapes:
     300 decode steps, G=256 HBM blocks, C=2048 host blocks, Poisson(4)
     arrivals, prompts U[64,512], outputs U[32,512], GPU-first allocation with
@@ -206,10 +210,12 @@ def test_continuous_batching_simulation(gpu, fused, planner):
     G+C pool written with the same KV, and every slot written bit-exact. S
     rows through the fused launch and through two partials + merge, with the
     step planned on the host (one device-to-host copy per step, as in the
-    reference) or on the GPU (none)."""
+    reference) or on the GPU (none); and the fused launch with 60% of each
+    row's host blocks reduced by the host cores (hybrid split)."""
     from tests.simulate import run_simulation
 
-    stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused, planner=planner)
+    stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused, planner=planner,
+                           cpu_fraction=cpu_fraction)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
     assert stats["decode_rows"] > 1000

@@ -1,0 +1,113 @@
+"""GPU parity of the hybrid split decode (ops.hybrid_split_decode): the host
+tier shared between the GPU's fused launch and the host cores, the two fp32
+partials LSE-merged on the GPU.
+
+Checked against the float64 oracle (merge of the two tiers' float64 partials,
+as in test_gpu_split_fused) for host-core shares from 0 (all on the GPU) to 1
+(the reference's division: the host cores compute the whole host-tier
+partial, fastdecode/backend.py:343-351). Bars: fp32 out max-abs <= 2e-3, lse
+<= 1e-4 relative; 16-bit out fp16 2e-3 / bf16 1.6e-2; empty rows exactly 0 /
+-inf. Host-tier KV written on the stream by the GPU just before the call is
+seen by the host cores.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.test_gpu_split_fused import TOL16, oracle_merged, two_tier_case
+from vllm_fastdecoder_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def run_hybrid(c, dev, frac, out_dtype=torch.float32, threads=0):
+    q = c["q"].to(dev)
+    n, H, D = q.shape
+    out = torch.empty(n, H, D, dtype=out_dtype, device=dev)
+    lse = torch.empty(H, n, dtype=torch.float32, device=dev)
+    ops.hybrid_split_decode(q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"],
+                            c["hk"], c["hv"], c["bt_c"], c["len_c"], c["scale"], frac,
+                            out=out, lse=lse, num_threads=threads)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def check(out, lse, ref_o, ref_l, lens, tol=2e-3):
+    nz = lens > 0
+    o = out.double().cpu()
+    assert float((o[nz] - ref_o[nz]).abs().max()) <= tol
+    rel = (lse.double().cpu()[:, nz] - ref_l[:, nz]).abs() / ref_l[:, nz].abs().clamp(min=1)
+    assert float(rel.max()) <= 1e-4
+    assert torch.all(out.cpu()[~nz] == 0)
+    assert torch.all(torch.isneginf(lse.cpu()[:, ~nz]))
+
+
+@pytest.mark.parametrize("frac", [0.0, 0.3, 0.65, 1.0])
+@pytest.mark.parametrize("H,KVH,D,dtype", [(32, 32, 128, torch.float16),
+                                           (32, 8, 128, torch.bfloat16),
+                                           (16, 2, 64, torch.float16),
+                                           (8, 8, 256, torch.bfloat16)])
+def test_hybrid_matches_oracle(gpu, frac, H, KVH, D, dtype):
+    c = two_tier_case(12, H, KVH, D, dtype, seed=H + D + int(frac * 10), dev=gpu)
+    ref_o, ref_l = oracle_merged(c)
+    out, lse = run_hybrid(c, gpu, frac)
+    check(out, lse, ref_o, ref_l, c["lens"])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_hybrid_16bit_out_and_interleaved_tiers(gpu, dtype):
+    """Output in the KV dtype; tiers interleaved, each ending in a partial
+    block."""
+    c = two_tier_case(9, 16, 4, 128, dtype, seed=77, dev=gpu, gpu_first=False)
+    ref_o, ref_l = oracle_merged(c)
+    out, lse = run_hybrid(c, gpu, 0.5, out_dtype=dtype)
+    tol = TOL16[dtype]
+    nz = c["lens"] > 0
+    err = (out.double().cpu()[nz] - ref_o[nz]).abs() - tol * ref_o[nz].abs()
+    assert float(err.max()) <= tol
+    rel = (lse.double().cpu()[:, nz] - ref_l[:, nz]).abs() / ref_l[:, nz].abs().clamp(min=1)
+    assert float(rel.max()) <= 1e-4
+
+
+def test_hybrid_close_to_fused(gpu):
+    """Same inputs through the fused launch alone: the merge of two fp32
+    partials differs from the single-pass result by summation order only."""
+    from tests.test_gpu_split_fused import run_fused
+
+    c = two_tier_case(16, 32, 8, 128, torch.bfloat16, seed=5, dev=gpu)
+    o_f, l_f = run_fused(c, gpu)
+    nz = (c["lens"] > 0).to(gpu)
+    for frac in (0.4, 0.9):
+        o_h, l_h = run_hybrid(c, gpu, frac, threads=3)
+        assert float((o_h - o_f).abs().max()) <= 2e-5
+        assert float((l_h[:, nz] - l_f[:, nz]).abs().max()) <= 2e-5
+        assert torch.equal(l_h[:, ~nz], l_f[:, ~nz])  # empty rows: -inf in both
+
+
+def test_hybrid_sees_kv_written_by_the_gpu(gpu):
+    """The step's new token is written into the pinned host tier by the GPU
+    (reshape_and_cache on the stream) and then read by the host cores."""
+    c = two_tier_case(6, 8, 2, 64, torch.float16, seed=3, dev=gpu, special=False)
+    BS, D = 16, 64
+    q = c["q"]
+    n = q.shape[0]
+    g = torch.Generator().manual_seed(11)
+    k_new = torch.randn(n, 2, D, generator=g).to(torch.float16)
+    v_new = torch.randn(n, 2, D, generator=g).to(torch.float16)
+    slots = torch.full((n,), -1, dtype=torch.int64)
+    for i in range(n):
+        lc = int(c["len_c"][i])
+        if lc:
+            blk = int(c["bt_c"][i, (lc - 1) // BS])
+            slots[i] = blk * BS + (lc - 1) % BS
+    ops.reshape_and_cache(k_new.to(gpu), v_new.to(gpu), c["hk"].transpose(1, 2),
+                          c["hv"].transpose(1, 2), slots.to(gpu))
+    out, lse = run_hybrid(c, gpu, 1.0)  # the host cores read every host block
+    for i in range(n):  # the oracle sees the same writes
+        if slots[i] >= 0:
+            b, t = divmod(int(slots[i]), BS)
+            assert torch.equal(c["hk"][b, :, t], k_new[i]) and torch.equal(c["hv"][b, :, t], v_new[i])
+    ref_o, ref_l = oracle_merged(c)
+    check(out, lse, ref_o, ref_l, c["lens"])

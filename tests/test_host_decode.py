@@ -1,0 +1,183 @@
+"""Parity of the host-core partial decode (fd_host_decode_partial /
+ops.host_decode_attn) against the float64 oracle. Runs on the CPU.
+
+The host cores compute the reference's decode_attn (fastdecode/csrc/
+cpu_attn.cpp:298-411) over host-memory caches, so the tolerances are the GPU
+partial's:
+  * fp32 output: max |out - oracle| <= 2e-3 (16-bit KV, fp32 accumulation);
+  * output in the KV dtype: fp16 2e-3, bf16 1.6e-2 (atol and rtol, the
+    reference's tests/test_cpu_kernel.py:53), fp32 KV 1e-5;
+  * lse: |lse - oracle| <= 1e-4 * max(1, |oracle|);
+  * empty rows: out exactly 0, lse exactly -inf; range errors: NaN rows.
+Work items are independent, so results are bit-identical for every thread
+count.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from tests import cases
+from vllm_fastdecoder_amd import _lib, ops
+
+OUT_TOL_16BIT = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}
+
+
+def run(q, kc, vc, bt, lens, scale, out_dtype, threads=0):
+    n, H, D = q.shape
+    out = torch.full((n, H, D), 7.0, dtype=out_dtype)
+    lse = torch.full((H, n), 7.0, dtype=torch.float32)
+    ops.host_decode_attn(q, kc, vc, bt, lens, scale, out, lse, num_threads=threads)
+    return out, lse
+
+
+def check(out, lse, ref_out, ref_lse, lens, kv_dtype):
+    nz = lens > 0
+    o = out.double()
+    if out.dtype == torch.float32 and kv_dtype != torch.float32:
+        err = float((o[nz] - ref_out[nz]).abs().max()) if nz.any() else 0.0
+        assert err <= 2e-3, err
+    else:
+        tol = OUT_TOL_16BIT[kv_dtype]
+        if nz.any():
+            err = float(((o[nz] - ref_out[nz]).abs() - tol * ref_out[nz].abs()).max())
+            assert err <= tol, err
+    if nz.any():
+        lerr = (lse.double()[:, nz] - ref_lse[:, nz]).abs() / ref_lse[:, nz].abs().clamp(min=1.0)
+        assert float(lerr.max()) <= 1e-4, float(lerr.max())
+    assert torch.all(out[~nz] == 0)
+    assert torch.all(torch.isneginf(lse[:, ~nz]))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H,KVH", [(8, 8), (8, 2), (4, 1), (6, 2), (12, 2), (16, 1), (7, 1)])
+@pytest.mark.parametrize("D", [64, 128, 72, 20])
+def test_host_decode_matches_oracle(dtype, H, KVH, D):
+    """The reference's kernel grid (tests/test_cpu_kernel.py:38-57), plus
+    query-head groups that are not powers of two or exceed 8 (several passes
+    over the KV) and head sizes that are not multiples of 8 or 16."""
+    n, BS, C = 7, 16, 64
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=93, seed=D + H)
+    lens[3] = 0
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    for out_dtype in (dtype, torch.float32):
+        out, lse = run(q, kc, vc, bt, lens, scale, out_dtype)
+        check(out, lse, ref_out, ref_lse, lens, dtype)
+
+
+@pytest.mark.parametrize("BS", [1, 4, 8, 32])
+def test_host_decode_block_sizes(BS):
+    dtype = torch.bfloat16
+    q, kc, vc, bt, lens = cases.rand_case(5, 8, 2, 128, BS, 200, dtype, max_len=150, seed=BS)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, 0.09)
+    out, lse = run(q, kc, vc, bt, lens, 0.09, torch.float32)
+    check(out, lse, ref_out, ref_lse, lens, dtype)
+
+
+def test_host_decode_large_scores():
+    """q x 300: the running max keeps every value finite
+    (test_cpu_kernel.py:60-72)."""
+    for dtype, D in ((torch.float32, 64), (torch.float16, 128)):
+        q, kc, vc, bt, lens = cases.rand_case(2, 4, 4, D, 16, 8, torch.float32, 40, 0)
+        q = (q * 300.0).to(dtype)
+        kc, vc = kc.to(dtype), vc.to(dtype)
+        ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, 1.0)
+        out, lse = run(q, kc, vc, bt, lens, 1.0, torch.float32)
+        assert torch.isfinite(out).all() and torch.isfinite(lse).all()
+        assert float((out.double() - ref_out).abs().max()) <= (1e-3 if dtype == torch.float16
+                                                               else 1e-4)
+        assert float((lse.double() - ref_lse).abs().max()) <= 1e-3 * float(ref_lse.abs().max())
+
+
+def test_host_decode_matches_reference_cpu_kernel_restatement():
+    """Against the oracle's fp32 two-pass restatement of cpu_attn.cpp:298-411
+    on the correctness workload shape (n=8, 32/32 heads, D=128, fp16)."""
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    k, v, _ = cases.kv_pool(w, pool, "host", "cpu")
+    q = cases.queries(w, "cpu")
+    n, H, D = q.shape
+    ref_o = torch.empty(n, H, D)
+    ref_l = torch.empty(H, n)
+    oracle.decode_attn_cpu_f32(q, k, v, bt.contiguous(), lens, w.scale, ref_o, ref_l)
+    out, lse = run(q, k, v, bt, lens, w.scale, torch.float32)
+    assert float((out - ref_o).abs().max()) <= 2e-3
+    assert float(((lse - ref_l).abs() / ref_l.abs().clamp(min=1)).max()) <= 1e-4
+
+
+def test_host_decode_thread_counts_bit_identical():
+    q, kc, vc, bt, lens = cases.rand_case(23, 8, 2, 128, 16, 300, torch.float16, 400, 9)
+    base = run(q, kc, vc, bt, lens, 0.1, torch.float32, threads=1)
+    for t in (2, 3, 8, 64):
+        o, l = run(q, kc, vc, bt, lens, 0.1, torch.float32, threads=t)
+        assert torch.equal(o, base[0]) and torch.equal(l, base[1]), t
+    assert _lib.load_lib().fd_host_decode_threads() >= 1
+
+
+def test_host_decode_strided_views_and_padded_table():
+    """q and out as head-major views, the table padded with junk past each
+    row's blocks (never read), the caches as halves of one buffer."""
+    n, H, KVH, D, BS, C = 6, 8, 4, 64, 16, 40
+    q0, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float16, 120, 4)
+    kv = torch.stack([kc, vc], dim=0)  # [2, C, KVH, BS, D]
+    qbuf = torch.zeros(H, n, D, dtype=torch.float16)
+    qbuf.copy_(q0.transpose(0, 1))
+    q = qbuf.transpose(0, 1)  # strides (D, n*D, 1)
+    btp = torch.randint(-(10**6), 10**6, (n, bt.shape[1] + 5), dtype=torch.int32)
+    for i in range(n):
+        nb = (int(lens[i]) + BS - 1) // BS
+        btp[i, :nb] = bt[i, :nb]
+    obuf = torch.zeros(H, n, D, dtype=torch.float32)
+    out = obuf.transpose(0, 1)
+    lse = torch.empty(H, n)
+    ops.host_decode_attn(q, kv[0], kv[1], btp, lens, 0.125, out, lse)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q0, kc, vc, bt, lens, 0.125)
+    check(out, lse, ref_out, ref_lse, lens, torch.float16)
+
+
+def test_host_decode_range_errors_give_nan_rows():
+    n, H, KVH, D, BS, C = 4, 4, 2, 64, 16, 20
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.bfloat16, 64, 1)
+    lens = torch.tensor([64, 30, 17, 5], dtype=torch.int32)
+    bt = torch.tensor([[0, 1, 2, 3], [4, C, 0, 0], [6, 7, 0, 0], [-1, 0, 0, 0]], dtype=torch.int32)
+    bad_lens = lens.clone()
+    bad_lens[2] = 4 * BS + 1  # past the table
+    out, lse = run(q, kc, vc, bt, bad_lens, 0.1, torch.bfloat16)
+    ok = torch.tensor([True, False, False, False])
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q[ok], kc, vc, bt[ok], lens[ok], 0.1)
+    check(out[ok], lse[:, ok], ref_out, ref_lse, lens[ok], torch.bfloat16)
+    assert torch.isnan(out[~ok]).all() and torch.isnan(lse[:, ~ok]).all()
+
+
+def test_host_decode_rejects_bad_arguments():
+    q, kc, vc, bt, lens = cases.rand_case(2, 4, 2, 64, 16, 8, torch.float16, 30, 0)
+    out = torch.empty(2, 4, 64)
+    lse = torch.empty(4, 2)
+    with pytest.raises(RuntimeError, match="host memory"):
+        ops.host_decode_attn(q.to("meta"), kc, vc, bt, lens, 0.1, out, lse)
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        ops.host_decode_attn(q.float(), kc, vc, bt, lens, 0.1, out, lse)
+    with pytest.raises(RuntimeError, match="int32"):
+        ops.host_decode_attn(q, kc, vc, bt.long(), lens, 0.1, out, lse)
+    lib = _lib.load_lib()
+    st = lib.fd_host_decode_partial(
+        q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+        kc.stride(0), kc.stride(1), kc.stride(2), 8, bt.data_ptr(), bt.stride(0), bt.shape[1],
+        lens.data_ptr(), 2, 3, 2, 64, 16, 0.1, _lib.FD_F16, out.data_ptr(), out.stride(0),
+        out.stride(1), _lib.FD_F32, lse.data_ptr(), 2, 0)
+    assert st == _lib.FD_ERR_INVALID and b"bad sizes" in lib.fd_last_error()
+    st = lib.fd_host_decode_partial(
+        q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+        kc.stride(0), kc.stride(1), kc.stride(2), 8, bt.data_ptr(), bt.stride(0), bt.shape[1],
+        lens.data_ptr(), 2, 4, 2, 64, 16, 0.1, _lib.FD_F16, out.data_ptr(), out.stride(0),
+        out.stride(1), _lib.FD_BF16, lse.data_ptr(), 2, 0)
+    assert st == _lib.FD_ERR_INVALID and b"out dtype" in lib.fd_last_error()
+    # n == 0 is a no-op even with NULL buffers
+    assert lib.fd_host_decode_partial(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 0, 4,
+                                      2, 64, 16, 0.1, _lib.FD_F16, None, 0, 0, _lib.FD_F16,
+                                      None, 0, 0) == _lib.FD_OK

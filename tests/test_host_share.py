@@ -1,0 +1,72 @@
+"""plan.share_host_blocks: the division of each row's host-tier blocks
+between the GPU and the host cores (host logic, CPU only).
+
+Invariants checked on random tables: the GPU's leading blocks followed by the
+host cores' trailing blocks are exactly the row's block list; the two token
+counts add up to the row's; the GPU's count covers whole blocks whenever the
+host cores have any; the host cores get floor(nb * f + 1/2) blocks; f = 1 is
+the reference's division (every host block on the host cores) and f = 0
+leaves everything to the GPU.
+"""
+
+from __future__ import annotations
+
+import math
+import random
+
+import pytest
+import torch
+
+from vllm_fastdecoder_amd.plan import share_host_blocks
+
+
+def _random_rows(rng, n, BS, W):
+    lens = torch.tensor([rng.choice([0, 1, BS, rng.randint(1, W * BS)]) for _ in range(n)],
+                        dtype=torch.int32)
+    bt = torch.randint(-5, 10**6, (n, W), dtype=torch.int32)  # junk past each row's blocks
+    return bt, lens
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_share_invariants(seed):
+    rng = random.Random(seed)
+    BS = rng.choice([1, 4, 16])
+    n, W = rng.randint(1, 30), rng.randint(1, 40)
+    bt, lens = _random_rows(rng, n, BS, W)
+    f = rng.choice([0.0, 1.0, rng.random()])
+    s = share_host_blocks(bt, lens, BS, f)
+    assert s.gpu_lens.dtype == s.cpu_lens.dtype == s.cpu_bt.dtype == torch.int32
+    for r in range(n):
+        L = int(lens[r])
+        nb = (L + BS - 1) // BS
+        gl, cl = int(s.gpu_lens[r]), int(s.cpu_lens[r])
+        assert gl + cl == L
+        kc = (cl + BS - 1) // BS
+        assert kc == min(nb, math.floor(nb * f + 0.5))
+        if cl:
+            assert gl % BS == 0
+        kg = gl // BS if cl else (gl + BS - 1) // BS
+        assert kg + kc == nb
+        assert bt[r, :kg].tolist() + s.cpu_bt[r, :kc].tolist() == bt[r, :nb].tolist()
+        assert torch.all(s.cpu_bt[r, kc:] == 0)
+
+
+def test_share_extremes_are_the_reference_split_and_the_gpu_only_split():
+    bt = torch.tensor([[5, 6, 7, 8], [1, 2, 0, 0], [3, 0, 0, 0], [0, 0, 0, 0]], dtype=torch.int32)
+    lens = torch.tensor([50, 17, 3, 0], dtype=torch.int32)
+    s1 = share_host_blocks(bt, lens, 16, 1.0)
+    assert s1.gpu_lens.tolist() == [0, 0, 0, 0] and s1.cpu_lens.tolist() == [50, 17, 3, 0]
+    assert s1.cpu_bt[:, :4].tolist() == [[5, 6, 7, 8], [1, 2, 0, 0], [3, 0, 0, 0], [0, 0, 0, 0]]
+    s0 = share_host_blocks(bt, lens, 16, 0.0)
+    assert s0.gpu_lens.tolist() == [50, 17, 3, 0] and s0.cpu_lens.tolist() == [0, 0, 0, 0]
+    sh = share_host_blocks(bt, lens, 16, 0.5)
+    assert sh.gpu_lens.tolist() == [32, 16, 0, 0] and sh.cpu_lens.tolist() == [18, 1, 3, 0]
+    assert sh.cpu_bt.tolist() == [[7, 8], [2, 0], [3, 0], [0, 0]]
+
+
+def test_share_rejects_fractions_outside_unit_interval():
+    bt = torch.zeros(1, 1, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        share_host_blocks(bt, torch.ones(1, dtype=torch.int32), 16, 1.5)
+    s = share_host_blocks(bt[:0], torch.zeros(0, dtype=torch.int32), 16, 0.5)
+    assert s.gpu_lens.numel() == 0 and s.cpu_bt.shape[0] == 0

@@ -18,7 +18,7 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class FdKvTier(ctypes.Structure):
@@ -122,6 +122,23 @@ SIGNATURES: dict[str, tuple] = {
     "fd_host_alloc": (c_int, [c_size_t, POINTER(c_void_p)]),
     "fd_host_free": (c_int, [c_void_p]),
     "fd_host_device_pointer": (c_int, [c_void_p, POINTER(c_void_p)]),
+    "fd_host_decode_partial": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64,            # q, q strides
+            c_void_p, c_void_p,                    # k_cache, v_cache
+            c_int64, c_int64, c_int64,             # kv strides block/head/token
+            c_int64,                               # num_blocks
+            c_void_p, c_int64, c_int32,            # block_table, bt_stride, bt_width
+            c_void_p,                              # lens
+            c_int32, c_int32, c_int32, c_int32,    # n, H, KVH, D
+            c_int32, c_float, c_int32,             # block_size, scale, kv_dtype
+            c_void_p, c_int64, c_int64, c_int32,   # out, strides, out_dtype
+            c_void_p, c_int64,                     # lse, lse_stride_head
+            c_int32,                               # num_threads
+        ],
+    ),
+    "fd_host_decode_threads": (c_int, []),
     "fd_stream_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 

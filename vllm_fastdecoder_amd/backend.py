@@ -185,6 +185,11 @@ class SplitDecodeImpl:
     # S rows through one fused launch (OPS.split_decode) instead of two
     # partials and a merge; the unfused path is the reference's contract
     fused_split: bool = True
+    # share of each S row's host-tier blocks reduced by the host cores while
+    # the GPU reads the rest over the link (ops.hybrid_split_begin; fused path
+    # only). 0 = the GPU reads the whole host tier; 1 = the reference's
+    # division (the host cores compute the whole host-tier partial).
+    cpu_fraction: float = 0.0
 
     def _forward_split(self, layer, query, key, value, kv_cache, dp: DevicePlan, output):
         """query [T, H, D]; key/value [T, KVH, D] (possibly strided views);
@@ -215,7 +220,15 @@ class SplitDecodeImpl:
         #    back as (0, -inf) from the kernel, so every S row goes in as is.
         ns = hp.n_s
         fused = self.fused_split and getattr(OPS, "split_decode", None) is not None
-        if ns and fused:
+        hybrid = None
+        if ns and fused and self.cpu_fraction > 0:
+            # the GPU's share is enqueued now; the host cores run after the P
+            # and F launches below, so those queue behind it on the GPU
+            qs = query.index_select(0, dp.s_tok)
+            hybrid = ops.hybrid_split_begin(qs, key_cache, value_cache, dp.s_gpu_bt_all,
+                                            hp.s_gpu_lens, k_host, v_host, hp.s_cpu_bt,
+                                            hp.s_cpu_lens, float(self.scale), self.cpu_fraction)
+        elif ns and fused:
             qs = query.index_select(0, dp.s_tok)
             merged, _ = OPS.split_decode(qs, key_cache, value_cache, dp.s_gpu_bt_all,
                                          dp.s_gpu_lens_all, k_host, v_host, dp.s_cpu_bt,
@@ -261,6 +274,8 @@ class SplitDecodeImpl:
             output.index_copy_(0, dp.f_tok, o_f)
 
         # 4) merge the split decodes' partials into their output rows
+        if hybrid is not None:
+            merged, _ = hybrid.finish()
         if ns:
             if not fused:
                 merged = torch.empty_like(qs)

@@ -2,7 +2,9 @@
 
 The library is compiled in-tree with hipcc (no JIT cache), so the built
 shared object sits next to this file and ships with the package. Every HIP
-source under csrc/ is compiled for gfx950 only.
+source under csrc/ is compiled for gfx950 only; the host-only C++ sources
+(the host-core decode of the host tier) are compiled with the system C++
+compiler and linked into the same library.
 """
 
 from __future__ import annotations
@@ -31,8 +33,19 @@ HIPCC_FLAGS = [
 ]
 
 
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wno-unused-function"]
+
+
 def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
+
+
+def host_sources() -> list[Path]:
+    return sorted(CSRC.glob("*.cpp"))
+
+
+def cxx() -> str:
+    return os.environ.get("CXX", "g++")
 
 
 def hipcc() -> str:
@@ -46,7 +59,7 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
+        raise RuntimeError(f"{cmd[0]} failed ({res.returncode}):\n{res.stderr}")
     if verbose and res.stderr:
         # hipcc's host pass warns about the device-only target feature
         lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
@@ -60,16 +73,21 @@ def build(verbose: bool = False, out: Path | None = None) -> Path:
     out = out or LIB_PATH
     tmp = out.with_suffix(".so.tmp")
     srcs = sources()
-    jobs = max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    hsrcs = host_sources()
+    jobs = max(1, min(len(srcs) + len(hsrcs),
+                      int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with tempfile.TemporaryDirectory(prefix="fdattn_build_") as d:
         objs = [Path(d) / (src.stem + ".o") for src in srcs]
+        hobjs = [Path(d) / (src.stem + ".host.o") for src in hsrcs]
         cmds = [[hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
                 for src, obj in zip(srcs, objs)]
+        cmds += [[cxx(), *CXX_FLAGS, "-c", str(src), "-o", str(obj)]
+                 for src, obj in zip(hsrcs, hobjs)]
         with ThreadPoolExecutor(max_workers=jobs) as pool:
             for f in [pool.submit(_run, c, verbose) for c in cmds]:
                 f.result()
-        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", *map(str, objs),
-              "-o", str(tmp)], verbose)
+        _run([hipcc(), f"--offload-arch={ARCH}", "-fPIC", "-shared", "-pthread",
+              *map(str, objs + hobjs), "-o", str(tmp)], verbose)
     os.replace(tmp, out)
     return out
 

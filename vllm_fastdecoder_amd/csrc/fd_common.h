@@ -7,14 +7,13 @@
 #include <stdint.h>
 
 #include "../../include/fdattn.h"
+#include "fd_errors.h"
 
 namespace fd {
 
 constexpr int kWave = 64;
 
 // ---------------------------------------------------------------- errors
-// Records a printf-style message for fd_last_error() and returns `code`.
-int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 // Converts a failed HIP call into FD_ERR_HIP with the runtime's message.
 int hip_error(hipError_t e, const char* what);
 

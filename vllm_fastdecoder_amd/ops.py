@@ -23,6 +23,7 @@ import torch
 from . import _lib
 from .pinned import device_ptr
 from .plan import longest_first as _longest_first
+from .plan import share_host_blocks as _share_host_blocks
 
 _DT = {torch.float16: _lib.FD_F16, torch.bfloat16: _lib.FD_BF16, torch.float32: _lib.FD_F32}
 
@@ -255,6 +256,139 @@ def split_decode(
     return out, lse
 
 
+class HybridSplit:
+    """A hybrid split decode in flight (hybrid_split_begin): the GPU's share
+    is enqueued; finish() runs the host cores' share and enqueues the merge."""
+
+    def __init__(self, out, lse, o_gpu, l_gpu, q_host, q_ready, host_k_cache, host_v_cache,
+                 share, softmax_scale, num_threads):
+        self.out, self.lse = out, lse
+        self._o_gpu, self._l_gpu = o_gpu, l_gpu
+        self._q_host, self._q_ready = q_host, q_ready
+        self._hk, self._hv = host_k_cache, host_v_cache
+        self._share = share
+        self._scale = softmax_scale
+        self._threads = num_threads
+        self.cpu_seconds = 0.0  # wall time of the host cores' share (0 before finish)
+
+    def finish(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """Waits for q on the host, reduces the host cores' blocks (blocking
+        the caller), uploads that partial and enqueues the merge."""
+        if self._o_gpu is None:
+            return self.out, self.lse
+        import time
+
+        dev = self.out.device
+        n, H, D = self.out.shape
+        o_cpu = torch.empty(n, H, D, dtype=torch.float32, pin_memory=True)
+        l_cpu = torch.empty(H, n, dtype=torch.float32, pin_memory=True)
+        self._q_ready.synchronize()
+        t0 = time.perf_counter()
+        host_decode_attn(self._q_host, self._hk, self._hv, self._share.cpu_bt,
+                         self._share.cpu_lens, self._scale, o_cpu, l_cpu,
+                         num_threads=self._threads)
+        self.cpu_seconds = time.perf_counter() - t0
+        merge_attn_states(self.out, self._o_gpu, self._l_gpu, o_cpu.to(dev, non_blocking=True),
+                          l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
+        self._o_gpu = self._l_gpu = self._q_host = None
+        return self.out, self.lse
+
+
+def hybrid_split_begin(
+    q: torch.Tensor,
+    hbm_key_cache: torch.Tensor,
+    hbm_value_cache: torch.Tensor,
+    hbm_block_table: torch.Tensor,
+    hbm_lens: torch.Tensor,
+    host_k_cache: torch.Tensor,
+    host_v_cache: torch.Tensor,
+    host_block_table: torch.Tensor,
+    host_lens: torch.Tensor,
+    softmax_scale: float,
+    cpu_fraction: float,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+    num_threads: int = 0,
+) -> HybridSplit:
+    """First half of hybrid_split_decode: divides the host tier, starts the
+    copy of q to the host and enqueues the GPU's fused launch. Other GPU work
+    can be enqueued before HybridSplit.finish()."""
+    _require(q.is_cuda and q.dim() == 3, "q must be [n, H, D] on the GPU")
+    _require(host_block_table.device.type == "cpu" and host_lens.device.type == "cpu",
+             "host_block_table and host_lens must be CPU tensors")
+    _require(host_k_cache.device.type == "cpu" and host_v_cache.device.type == "cpu",
+             "the host tier must be in host memory")
+    n, H, D = q.shape
+    dev = q.device
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty(H, n, dtype=torch.float32, device=dev)
+    share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
+    if n == 0:
+        return HybridSplit(out, lse, None, None, None, None, host_k_cache, host_v_cache, share,
+                           softmax_scale, num_threads)
+    q_host = torch.empty(q.shape, dtype=q.dtype, pin_memory=True)
+    q_host.copy_(q, non_blocking=True)
+    q_ready = torch.cuda.Event()
+    q_ready.record(torch.cuda.current_stream(dev))
+
+    def up(t):  # host index tensors: pinned, asynchronous upload
+        return t if t.is_cuda else t.pin_memory().to(dev, non_blocking=True)
+
+    # rows by decreasing GPU work when the HBM lengths are known on the host
+    order = None if hbm_lens.is_cuda else up(_longest_first(hbm_lens + share.gpu_lens))
+    o_gpu = torch.empty(n, H, D, dtype=torch.float32, device=dev)
+    l_gpu = torch.empty(H, n, dtype=torch.float32, device=dev)
+    split_decode(q, hbm_key_cache, hbm_value_cache, up(hbm_block_table), up(hbm_lens),
+                 host_k_cache, host_v_cache, up(host_block_table), up(share.gpu_lens),
+                 softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
+    return HybridSplit(out, lse, o_gpu, l_gpu, q_host, q_ready, host_k_cache, host_v_cache,
+                       share, softmax_scale, num_threads)
+
+
+def hybrid_split_decode(
+    q: torch.Tensor,
+    hbm_key_cache: torch.Tensor,
+    hbm_value_cache: torch.Tensor,
+    hbm_block_table: torch.Tensor,
+    hbm_lens: torch.Tensor,
+    host_k_cache: torch.Tensor,
+    host_v_cache: torch.Tensor,
+    host_block_table: torch.Tensor,
+    host_lens: torch.Tensor,
+    softmax_scale: float,
+    cpu_fraction: float,
+    out: torch.Tensor | None = None,
+    lse: torch.Tensor | None = None,
+    num_threads: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """split_decode with the host tier shared between the GPU and the host
+    cores: the reference's split step (fastdecode/backend.py:293-356: GPU
+    partial, host-core partial of the host tier, merge) with part of the host
+    tier moved back to the GPU.
+
+    Each row's host blocks are divided by plan.share_host_blocks: the GPU's
+    fused launch reads the HBM tier plus the leading host blocks over the
+    link; meanwhile the host cores (fd_host_decode_partial) reduce the
+    trailing ones from their own DRAM; the two fp32 partials are LSE-merged
+    on the GPU. cpu_fraction 1 is the reference's division of work, 0 is
+    split_decode. host_block_table / host_lens must be CPU tensors (the
+    host-side planner's s_cpu_bt / s_cpu_lens); the other arguments are those
+    of split_decode (tables and lengths on the host are uploaded
+    asynchronously).
+
+    Synchronises the host with the GPU once, for the copy of q to the host
+    (which is ordered before the fused launch, so the wait does not include
+    it), and blocks the caller while the host cores run. Host-tier KV written
+    by earlier work on the stream is visible to the host cores.
+    """
+    return hybrid_split_begin(q, hbm_key_cache, hbm_value_cache, hbm_block_table, hbm_lens,
+                              host_k_cache, host_v_cache, host_block_table, host_lens,
+                              softmax_scale, cpu_fraction, out=out, lse=lse,
+                              num_threads=num_threads).finish()
+
+
 def plan_tiers(block_table: torch.Tensor, seq_lens: torch.Tensor, slot_mapping: torch.Tensor,
                num_gpu_blocks: int, num_cpu_blocks: int, block_size: int,
                error_count: torch.Tensor | None = None):
@@ -326,6 +460,56 @@ def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse, row_ord
     paged_decode_partial(
         q, k_cache, v_cache, (k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)),
         C, BS, KVH, block_table, lens, scale, out, lse, row_order=row_order,
+    )
+
+
+def host_decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse,
+                     num_threads: int = 0) -> None:
+    """Host-tier partial computed by the host cores (fd_host_decode_partial):
+    the signature and results of decode_attn above, i.e. of the reference's
+    decode_attn (fastdecode/csrc/cpu_attn.cpp:456-489), with every tensor in
+    host memory. Runs synchronously; num_threads 0 = one worker per CPU of
+    the affinity mask (or FASTDECODE_CPU_THREADS)."""
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
+                    ("block_table", block_table), ("lens", lens), ("out", out), ("lse", lse)):
+        _require(t.device.type == "cpu", f"{name} must be in host memory")
+    _require(k_cache.dim() == 4 and v_cache.shape == k_cache.shape
+             and k_cache.stride() == v_cache.stride(), "k_cache/v_cache must be [C, KVH, BS, D]")
+    C, KVH, BS, D = k_cache.shape
+    _require(q.dim() == 3 and q.shape[2] == D and out.shape == q.shape,
+             "q and out must be [n, H, D] with the cache's head size")
+    n, H = q.shape[0], q.shape[1]
+    _require(H % KVH == 0, "num_heads must be a multiple of num_kv_heads")
+    _require(k_cache.stride(3) == 1 and q.stride(2) == 1 and out.stride(2) == 1,
+             "head_size must be the contiguous dim")
+    kv_dt = _dtype_code(k_cache, "k_cache")
+    _require(q.dtype == k_cache.dtype and v_cache.dtype == k_cache.dtype,
+             "q, k_cache and v_cache must share a dtype")
+    _require(out.dtype == q.dtype or out.dtype == torch.float32, "out must be q's dtype or float32")
+    _require(lse.dtype == torch.float32 and tuple(lse.shape) == (H, n)
+             and (n == 0 or lse.stride(1) == 1), "lse must be float32 [H, n]")
+    _require(block_table.dtype == torch.int32 and lens.dtype == torch.int32
+             and block_table.dim() == 2 and block_table.shape[0] == n and lens.shape == (n,),
+             "block_table must be int32 [n, W] and lens int32 [n]")
+    if n == 0:
+        return
+    _require(block_table.stride(1) == 1, "block_table rows must be contiguous")
+    lens = lens.contiguous()
+    lib = _lib.load_lib()
+    _lib.check(
+        lib.fd_host_decode_partial(
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k_cache.data_ptr(), v_cache.data_ptr(),
+            k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+            C,
+            block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            lens.data_ptr(),
+            n, H, KVH, D,
+            BS, float(scale), kv_dt,
+            out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
+            lse.data_ptr(), lse.stride(0),
+            int(num_threads),
+        )
     )
 
 

@@ -271,3 +271,40 @@ def to_device(hp: HostPlan, block_table_dev: torch.Tensor, device) -> DevicePlan
         s_cpu_order=d(longest_first(hp.s_cpu_lens)),
         s_order=d(longest_first(hp.s_gpu_lens + hp.s_cpu_lens)),
     )
+
+
+@dataclass
+class HostShare:
+    """How one step's host-tier blocks are divided between the GPU (reading
+    them over the link) and the host cores (reading their own DRAM)."""
+
+    gpu_lens: torch.Tensor  # [n] int32 host-tier tokens the GPU reads: whole leading blocks
+    cpu_bt: torch.Tensor  # [n, Wc] int32 the host cores' blocks: each row's trailing ones
+    cpu_lens: torch.Tensor  # [n] int32
+
+
+def share_host_blocks(host_bt: torch.Tensor, host_lens: torch.Tensor, block_size: int,
+                      cpu_fraction: float) -> HostShare:
+    """Gives the last round(cpu_fraction * nb) of each row's nb host-tier
+    blocks (the partial last block among them; halves round up) to the host cores and the
+    leading ones to the GPU. cpu_fraction 1 is the reference's split (the
+    host cores compute the whole host-tier partial, fastdecode/backend.py:
+    343-351); 0 leaves everything to the GPU. The GPU keeps its rows' table
+    (its length covers only whole leading blocks); the host cores get each
+    row's trailing ids shifted to column 0, zero padded. CPU tensors in and
+    out."""
+    if not 0.0 <= cpu_fraction <= 1.0:
+        raise ValueError(f"cpu_fraction must be in [0, 1], got {cpu_fraction}")
+    lens = host_lens.to(torch.int64).clamp(min=0)
+    n, W = host_bt.shape
+    nb = (lens + block_size - 1) // block_size
+    k_cpu = torch.minimum(torch.floor(nb.double() * cpu_fraction + 0.5).to(torch.int64), nb)
+    j0 = nb - k_cpu
+    gpu_lens = torch.where(k_cpu > 0, j0 * block_size, lens)
+    cpu_lens = lens - gpu_lens
+    wc = int(k_cpu.max()) if n else 0
+    cols = torch.arange(max(wc, 1), dtype=torch.int64)
+    src = (j0[:, None] + cols[None, :]).clamp(max=max(W - 1, 0))
+    cpu_bt = (host_bt.gather(1, src) if W else torch.zeros(n, cols.numel(), dtype=torch.int32))
+    cpu_bt = torch.where(cols[None, :] < k_cpu[:, None], cpu_bt, 0).to(torch.int32).contiguous()
+    return HostShare(gpu_lens.to(torch.int32), cpu_bt, cpu_lens.to(torch.int32))
