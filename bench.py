@@ -316,6 +316,23 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     fracs = (0.5, 0.6, 0.7, 0.8, 0.9)
     t_hybrid = {f: time_gpu(hybrid(f), host_steps, 1, stream) for f in fracs}
     f_best = min(t_hybrid, key=t_hybrid.get)
+    # the share balanced online (SplitDecodeImpl(cpu_fraction="auto"))
+    from vllm_fastdecoder_amd.plan import ShareTuner
+
+    tuner = ShareTuner()
+    auto_fracs = []
+
+    def hybrid_auto():
+        h = ops.hybrid_split_begin(q, kc_g, vc_g, bt_g_d, len_g, hk, hv, bt_c, len_c, w.scale,
+                                   tuner.fraction, out=h_out, lse=h_lse)
+        h.finish()
+        auto_fracs.append(tuner.fraction)
+        tuner.update(h.gpu_finished_first)
+
+    for _ in range(60):
+        hybrid_auto()
+    auto_fracs.clear()
+    t_auto = time_gpu(hybrid_auto, 20, 0, stream)
     t_hbm = time_gpu(hbm, steps, warmup, stream)
     t_host = time_gpu(host, host_steps, 1, stream)
     t_merge = time_gpu(merge, steps, warmup, stream)
@@ -343,6 +360,10 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "hybrid_best_cpu_fraction": f_best,
         "hybrid_best_step_ms": round(t_hybrid[f_best], 3),
         "hybrid_best_tokens_per_s": round(w.n / (t_hybrid[f_best] / 1e3 * LAYERS), 1),
+        "hybrid_auto_step_ms": round(t_auto, 3),
+        "hybrid_auto_cpu_fraction": [round(min(auto_fracs), 3), round(max(auto_fracs), 3)],
+        "hybrid_auto_tokens_per_s": round(w.n / (t_auto / 1e3 * LAYERS), 1),
+        "hybrid_auto_GBps": round((kv_hbm + kv_host) / (t_auto / 1e3) / 1e9, 1),
         "planner": planner,
         "note": ("host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not "
                  "`value`; host_cores = fd_host_decode_partial over the whole host tier; "

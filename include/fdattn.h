@@ -8,7 +8,11 @@
  *   1. paged partial decode attention over a subset of a sequence's KV
  *      blocks, emitting (out, lse);
  *   2. the log-sum-exp merge of two partials (GPU tier + host tier);
- *   3. the reshape_and_cache slot-mapping write into a paged KV cache.
+ *   3. the reshape_and_cache slot-mapping write into a paged KV cache;
+ *
+ * plus the reference's host-core kernel itself (fd_host_decode_partial, x86
+ * AVX-512/AVX2), so part of the host tier can be reduced by the host cores
+ * while the GPU reads the rest.
  *
  * The same kernels serve both tiers of the reference's G+C block space: the
  * HBM tier (vLLM's [num_blocks, block_size, kv_heads, 2*head_size] cache) and
@@ -20,7 +24,8 @@
  *   - All buffers are caller-owned; nothing is allocated, and outputs are
  *     written in place (cpu_attn.cpp:452-489 and :491-517 contract).
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream)
- *     and the call returns without synchronising.
+ *     and the call returns without synchronising (fd_host_decode_partial,
+ *     which takes no stream, runs on the host and returns when done).
  *   - Arguments are validated on the host before any launch; an invalid call
  *     returns a non-zero status, writes nothing, and leaves a message for
  *     fd_last_error() (mirrors the TORCH_CHECKs of cpu_attn.cpp:433-477 and the
@@ -322,6 +327,12 @@ int fd_host_decode_partial(
 /* Worker count fd_host_decode_partial uses when num_threads is 0. No
  * counterpart in the reference (it uses OpenMP's default team). */
 int fd_host_decode_threads(void);
+
+/* Vector width in bits fd_host_decode_partial uses on this CPU: 512
+ * (AVX-512F), 256 (AVX2; also when FASTDECODE_CPU_ISA=avx2), 0 (neither:
+ * the call fails with FD_ERR_UNSUPPORTED). No counterpart in the reference
+ * (its kernel is compiled for one ISA, cpu_attn.cpp:1-40). */
+int fd_host_decode_isa(void);
 
 /* ------------------------------------------------------------------------
  * Measurement helper: streams `bytes` (a multiple of 16) from src to dst with

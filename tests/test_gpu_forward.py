@@ -201,7 +201,7 @@ def test_hipops_fa_rejects_prefill_forms(gpu):
 
 @pytest.mark.parametrize("fused,planner,cpu_fraction",
                          [(True, "host", 0.0), (False, "host", 0.0), (True, "device", 0.0),
-                          (True, "host", 0.6)])
+                          (True, "host", 0.6), (True, "host", "auto")])
 def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
     """The config of the reference's GPU self-test at vicuna-7b head shapes:
     300 decode steps, G=256 HBM blocks, C=2048 host blocks, Poisson(4)

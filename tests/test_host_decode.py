@@ -27,6 +27,18 @@ from vllm_fastdecoder_amd import _lib, ops
 OUT_TOL_16BIT = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}
 
 
+@pytest.fixture(params=["widest", "avx2"])
+def isa(request, monkeypatch):
+    """Each case on the widest vector ISA of this CPU and on the AVX2 body."""
+    if request.param == "avx2":
+        monkeypatch.setenv("FASTDECODE_CPU_ISA", "avx2")
+        assert _lib.load_lib().fd_host_decode_isa() == 256
+    else:
+        monkeypatch.delenv("FASTDECODE_CPU_ISA", raising=False)
+        assert _lib.load_lib().fd_host_decode_isa() in (256, 512)
+    return request.param
+
+
 def run(q, kc, vc, bt, lens, scale, out_dtype, threads=0):
     n, H, D = q.shape
     out = torch.full((n, H, D), 7.0, dtype=out_dtype)
@@ -56,7 +68,7 @@ def check(out, lse, ref_out, ref_lse, lens, kv_dtype):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("H,KVH", [(8, 8), (8, 2), (4, 1), (6, 2), (12, 2), (16, 1), (7, 1)])
 @pytest.mark.parametrize("D", [64, 128, 72, 20])
-def test_host_decode_matches_oracle(dtype, H, KVH, D):
+def test_host_decode_matches_oracle(dtype, H, KVH, D, isa):
     """The reference's kernel grid (tests/test_cpu_kernel.py:38-57), plus
     query-head groups that are not powers of two or exceed 8 (several passes
     over the KV) and head sizes that are not multiples of 8 or 16."""
@@ -71,7 +83,7 @@ def test_host_decode_matches_oracle(dtype, H, KVH, D):
 
 
 @pytest.mark.parametrize("BS", [1, 4, 8, 32])
-def test_host_decode_block_sizes(BS):
+def test_host_decode_block_sizes(BS, isa):
     dtype = torch.bfloat16
     q, kc, vc, bt, lens = cases.rand_case(5, 8, 2, 128, BS, 200, dtype, max_len=150, seed=BS)
     ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, 0.09)
@@ -79,7 +91,7 @@ def test_host_decode_block_sizes(BS):
     check(out, lse, ref_out, ref_lse, lens, dtype)
 
 
-def test_host_decode_large_scores():
+def test_host_decode_large_scores(isa):
     """q x 300: the running max keeps every value finite
     (test_cpu_kernel.py:60-72)."""
     for dtype, D in ((torch.float32, 64), (torch.float16, 128)):
@@ -110,7 +122,7 @@ def test_host_decode_matches_reference_cpu_kernel_restatement():
     assert float(((lse - ref_l).abs() / ref_l.abs().clamp(min=1)).max()) <= 1e-4
 
 
-def test_host_decode_thread_counts_bit_identical():
+def test_host_decode_thread_counts_bit_identical(isa):
     q, kc, vc, bt, lens = cases.rand_case(23, 8, 2, 128, 16, 300, torch.float16, 400, 9)
     base = run(q, kc, vc, bt, lens, 0.1, torch.float32, threads=1)
     for t in (2, 3, 8, 64):
@@ -119,7 +131,7 @@ def test_host_decode_thread_counts_bit_identical():
     assert _lib.load_lib().fd_host_decode_threads() >= 1
 
 
-def test_host_decode_strided_views_and_padded_table():
+def test_host_decode_strided_views_and_padded_table(isa):
     """q and out as head-major views, the table padded with junk past each
     row's blocks (never read), the caches as halves of one buffer."""
     n, H, KVH, D, BS, C = 6, 8, 4, 64, 16, 40
@@ -140,7 +152,7 @@ def test_host_decode_strided_views_and_padded_table():
     check(out, lse, ref_out, ref_lse, lens, torch.float16)
 
 
-def test_host_decode_range_errors_give_nan_rows():
+def test_host_decode_range_errors_give_nan_rows(isa):
     n, H, KVH, D, BS, C = 4, 4, 2, 64, 16, 20
     q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.bfloat16, 64, 1)
     lens = torch.tensor([64, 30, 17, 5], dtype=torch.int32)

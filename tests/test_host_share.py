@@ -70,3 +70,38 @@ def test_share_rejects_fractions_outside_unit_interval():
         share_host_blocks(bt, torch.ones(1, dtype=torch.int32), 16, 1.5)
     s = share_host_blocks(bt[:0], torch.zeros(0, dtype=torch.int32), 16, 0.5)
     assert s.gpu_lens.numel() == 0 and s.cpu_bt.shape[0] == 0
+
+
+def test_share_tuner_converges_to_the_balanced_fraction():
+    """A modelled step: the host cores take f * B bytes at rate c, the GPU
+    (1 - f) * B at rate g; whoever finishes first is reported. The tuner
+    settles within one step of the balance point c / (c + g) and stays
+    there."""
+    from vllm_fastdecoder_amd.plan import ShareTuner
+
+    for c, g in ((175.0, 55.6), (40.0, 55.6), (300.0, 20.0)):
+        t = ShareTuner(start=0.5, step=0.01)
+        seen = []
+        for _ in range(200):
+            f = t.fraction
+            t.update(gpu_finished_first=(1 - f) / g < f / c)
+            seen.append(t.fraction)
+        star = c / (c + g)
+        assert all(abs(x - star) <= 0.011 for x in seen[-50:]), (c, g, seen[-5:])
+
+
+def test_share_tuner_bounds_and_backend_validation():
+    from vllm_fastdecoder_amd import backend
+    from vllm_fastdecoder_amd.plan import ShareTuner
+
+    t = ShareTuner(start=0.06, step=0.05, lo=0.05, hi=1.0)
+    assert t.update(True) == 0.05 and t.update(True) == 0.05
+    t = ShareTuner(start=0.99, step=0.05)
+    assert t.update(False) == 1.0
+    with pytest.raises(ValueError):
+        ShareTuner(start=2.0)
+    assert backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction="auto")._host_share() == 0.75
+    assert backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction=0.3)._host_share() == 0.3
+    for bad in (1.5, -0.1, "fast"):
+        with pytest.raises(ValueError):
+            backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction=bad)

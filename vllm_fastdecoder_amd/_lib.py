@@ -139,6 +139,7 @@ SIGNATURES: dict[str, tuple] = {
         ],
     ),
     "fd_host_decode_threads": (c_int, []),
+    "fd_host_decode_isa": (c_int, []),
     "fd_stream_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 

@@ -188,8 +188,21 @@ class SplitDecodeImpl:
     # share of each S row's host-tier blocks reduced by the host cores while
     # the GPU reads the rest over the link (ops.hybrid_split_begin; fused path
     # only). 0 = the GPU reads the whole host tier; 1 = the reference's
-    # division (the host cores compute the whole host-tier partial).
-    cpu_fraction: float = 0.0
+    # division (the host cores compute the whole host-tier partial); "auto" =
+    # balanced online from each step's finishing order (plan.ShareTuner).
+    cpu_fraction: float | str = 0.0
+
+    def __post_init__(self) -> None:
+        self._tuner = None
+        if self.cpu_fraction == "auto":
+            from .plan import ShareTuner
+
+            self._tuner = ShareTuner()
+        elif not isinstance(self.cpu_fraction, (int, float)) or not 0 <= self.cpu_fraction <= 1:
+            raise ValueError(f"cpu_fraction must be in [0, 1] or 'auto', got {self.cpu_fraction!r}")
+
+    def _host_share(self) -> float:
+        return self._tuner.fraction if self._tuner is not None else float(self.cpu_fraction)
 
     def _forward_split(self, layer, query, key, value, kv_cache, dp: DevicePlan, output):
         """query [T, H, D]; key/value [T, KVH, D] (possibly strided views);
@@ -221,13 +234,14 @@ class SplitDecodeImpl:
         ns = hp.n_s
         fused = self.fused_split and getattr(OPS, "split_decode", None) is not None
         hybrid = None
-        if ns and fused and self.cpu_fraction > 0:
+        share = self._host_share()
+        if ns and fused and share > 0:
             # the GPU's share is enqueued now; the host cores run after the P
             # and F launches below, so those queue behind it on the GPU
             qs = query.index_select(0, dp.s_tok)
             hybrid = ops.hybrid_split_begin(qs, key_cache, value_cache, dp.s_gpu_bt_all,
                                             hp.s_gpu_lens, k_host, v_host, hp.s_cpu_bt,
-                                            hp.s_cpu_lens, float(self.scale), self.cpu_fraction)
+                                            hp.s_cpu_lens, float(self.scale), share)
         elif ns and fused:
             qs = query.index_select(0, dp.s_tok)
             merged, _ = OPS.split_decode(qs, key_cache, value_cache, dp.s_gpu_bt_all,
@@ -276,6 +290,8 @@ class SplitDecodeImpl:
         # 4) merge the split decodes' partials into their output rows
         if hybrid is not None:
             merged, _ = hybrid.finish()
+            if self._tuner is not None:
+                self._tuner.update(hybrid.gpu_finished_first)
         if ns:
             if not fused:
                 merged = torch.empty_like(qs)

@@ -16,12 +16,14 @@
 // from an atomic counter to a persistent thread pool. Per block one online
 // softmax step in fp32 for the item's query heads: the block's scores, one
 // max / rescale per head, then P.V with the rescale folded into the
-// accumulator load. AVX2 FMAs with enough independent accumulator chains per
-// head group to cover the FMA latency, F16C / shift conversions of fp16 /
+// accumulator load. Vector FMAs with enough independent accumulator chains
+// per head group to cover the FMA latency, F16C / shift conversions of fp16 /
 // bf16 rows, and exp2 from a degree-6 polynomial for 2^f on [-0.5, 0.5]
 // (least-squares fit on Chebyshev nodes, relative error < 1e-7 in fp32) times
-// 2^n assembled in the exponent field. The vector code is compiled for
-// AVX2+FMA+F16C and entered only after a run-time check of the CPU.
+// 2^n assembled in the exponent field. One kernel body
+// (host_decode_kernel.h) is compiled for AVX-512 (16 lanes) and for AVX2 (8
+// lanes) and the widest one the CPU supports is picked at run time; the rest
+// of the library is built for baseline x86-64.
 #include <immintrin.h>
 #include <sched.h>
 #include <stdint.h>
@@ -170,225 +172,143 @@ uint16_t f32_to_bf16(float x) {
   return (uint16_t)(u >> 16);
 }
 
-// ---------------------------------------------------------------- vector
-#pragma GCC push_options
-#pragma GCC target("avx2,fma,f16c")
-
-inline __m256 exp2_ps(__m256 x) {
-  const __m256 lo = _mm256_set1_ps(-126.f);
-  const __m256 tiny = _mm256_cmp_ps(x, lo, _CMP_LT_OQ);  // includes -inf
-  // operand order keeps a NaN input NaN (min/max return the second operand)
-  x = _mm256_max_ps(lo, _mm256_min_ps(_mm256_set1_ps(127.f), x));
-  const __m256 n = _mm256_round_ps(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
-  const __m256 f = _mm256_sub_ps(x, n);
-  __m256 p = _mm256_set1_ps(1.533757683e-04f);
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(1.339986036e-03f));
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(9.618519534e-03f));
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(5.550328998e-02f));
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(2.402264661e-01f));
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(6.931472056e-01f));
-  p = _mm256_fmadd_ps(p, f, _mm256_set1_ps(1.000000001e+00f));
-  const __m256i e = _mm256_slli_epi32(_mm256_cvtps_epi32(n), 23);
-  const __m256 r = _mm256_castsi256_ps(_mm256_add_epi32(_mm256_castps_si256(p), e));
-  return _mm256_andnot_ps(tiny, r);
-}
-
-inline float exp2_1(float x) { return _mm256_cvtss_f32(exp2_ps(_mm256_set1_ps(x))); }
-
-inline float hsum(__m256 v) {
-  __m128 s = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
-  s = _mm_add_ps(s, _mm_movehl_ps(s, s));
-  s = _mm_add_ss(s, _mm_shuffle_ps(s, s, 0x55));
-  return _mm_cvtss_f32(s);
-}
-
-// 8 consecutive elements of storage type DT as fp32
-template <int DT>
-inline __m256 ld8(const void* p) {
-  if constexpr (DT == FD_F32) {
-    return _mm256_loadu_ps(static_cast<const float*>(p));
-  } else if constexpr (DT == FD_F16) {
-    return _mm256_cvtph_ps(_mm_loadu_si128(static_cast<const __m128i*>(p)));
-  } else {
-    const __m256i w = _mm256_cvtepu16_epi32(_mm_loadu_si128(static_cast<const __m128i*>(p)));
-    return _mm256_castsi256_ps(_mm256_slli_epi32(w, 16));
-  }
-}
-
 // Scratch of one worker.
 struct Scratch {
   std::vector<float> q, acc, s;
 };
 
-// Online-softmax partial of query heads kh*Gr + g0 .. + G-1 (Gr = H / KVH) of
-// sequence i over kv head kh. Returns false if the row is invalid (a length
-// past its table or a block id outside the cache).
-template <int DT, int G>
-bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
-  constexpr int elt = DT == FD_F32 ? 4 : 2;
-  constexpr int U = G >= 4 ? 1 : 4 / G;   // score chains per head
-  constexpr int CU = G >= 8 ? 1 : 8 / G;  // P.V chunks in flight
-  const int D = a.D, BS = a.BS, Gr = a.H / a.KVH;
-  const int D8 = D & ~7;
-  const int L = a.lens[i];
-  const int nb = (L + BS - 1) / BS;
-  if (nb > a.bt_width) return false;
-  w.q.resize((size_t)G * D);
-  w.acc.assign((size_t)G * D, 0.f);
-  w.s.resize((size_t)G * BS);
-  float* qf = w.q.data();
-  float* acc = w.acc.data();
-  float* s = w.s.data();
-  const float qs = a.scale * 1.4426950408889634f;  // scores in the log2 domain
-  for (int g = 0; g < G; ++g) {
-    const int64_t qb = (int64_t)i * a.q_ss + (int64_t)(kh * Gr + g0 + g) * a.q_sh;
-    for (int d = 0; d < D; ++d) qf[g * D + d] = load1(a.q, qb + d, a.dt) * qs;
+constexpr int kPrefetchBlocks = 1;  // how far ahead the next block's rows are prefetched
+
+// exp2 for x <= 127: 2^x = 2^n * 2^f with n = round(x), |f| <= 1/2, 2^f from
+// the polynomial below, 2^n added into the exponent field; x < -126
+// (including -inf) gives 0 and NaN stays NaN (operand order of min/max).
+#define FD_EXP2_POLY(fma, set1, f)                        \
+  fma(fma(fma(fma(fma(fma(set1(1.533757683e-04f), f,      \
+                          set1(1.339986036e-03f)), f,     \
+                      set1(9.618519534e-03f)), f,         \
+                  set1(5.550328998e-02f)), f,             \
+              set1(2.402264661e-01f)), f,                 \
+          set1(6.931472056e-01f)), f,                     \
+      set1(1.000000001e+00f))
+
+// ---------------------------------------------------------------- AVX2
+#pragma GCC push_options
+#pragma GCC target("avx2,fma,f16c")
+namespace isa_avx2 {
+
+struct V {
+  using T = __m256;
+  static constexpr int W = 8;
+  static T zero() { return _mm256_setzero_ps(); }
+  static T set1(float x) { return _mm256_set1_ps(x); }
+  static T load(const float* p) { return _mm256_loadu_ps(p); }
+  static void store(float* p, T x) { _mm256_storeu_ps(p, x); }
+  static T bcast(const float* p) { return _mm256_broadcast_ss(p); }
+  static T add(T a, T b) { return _mm256_add_ps(a, b); }
+  static T sub(T a, T b) { return _mm256_sub_ps(a, b); }
+  static T mul(T a, T b) { return _mm256_mul_ps(a, b); }
+  static T fma(T a, T b, T c) { return _mm256_fmadd_ps(a, b, c); }
+  static float hsum(T v) {
+    __m128 x = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+    x = _mm_add_ps(x, _mm_movehl_ps(x, x));
+    x = _mm_add_ss(x, _mm_shuffle_ps(x, x, 0x55));
+    return _mm_cvtss_f32(x);
   }
-  float m[G], l[G], alpha[G];
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
+  static T exp2(T x) {
+    const T lo = set1(-126.f);
+    const T tiny = _mm256_cmp_ps(x, lo, _CMP_LT_OQ);
+    x = _mm256_max_ps(lo, _mm256_min_ps(set1(127.f), x));
+    const T n = _mm256_round_ps(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    const T f = sub(x, n);
+    const T p = FD_EXP2_POLY(fma, set1, f);
+    const __m256i e = _mm256_slli_epi32(_mm256_cvtps_epi32(n), 23);
+    return _mm256_andnot_ps(tiny, _mm256_castsi256_ps(_mm256_add_epi32(_mm256_castps_si256(p), e)));
   }
-  const char* kbase = static_cast<const char*>(a.k);
-  const char* vbase = static_cast<const char*>(a.v);
-  const int32_t* row_bt = a.bt + (int64_t)i * a.bt_stride;
-  for (int b = 0; b < nb; ++b) {
-    const int64_t bid = row_bt[b];
-    if (bid < 0 || bid >= a.num_blocks) return false;
-    const int ntok = std::min(BS, L - b * BS);
-    const int64_t base = bid * a.sb + (int64_t)kh * a.sh;
-    if (b + 1 < nb) {  // the next block's rows, while this one computes
-      const int64_t nid = row_bt[b + 1];
-      if (nid >= 0 && nid < a.num_blocks) {
-        const int64_t nbase = nid * a.sb + (int64_t)kh * a.sh;
-        for (int t = 0; t < BS; ++t)
-          for (int off = 0; off < D * elt; off += 64) {
-            _mm_prefetch(kbase + (nbase + (int64_t)t * a.st) * elt + off, _MM_HINT_T0);
-            _mm_prefetch(vbase + (nbase + (int64_t)t * a.st) * elt + off, _MM_HINT_T0);
-          }
-      }
-    }
-    // scores
-    for (int t = 0; t < ntok; ++t) {
-      const char* kp = kbase + (base + (int64_t)t * a.st) * elt;
-      __m256 c[G][U];
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < U; ++u) c[g][u] = _mm256_setzero_ps();
-      int d = 0;
-      for (; d + 8 * U <= D8; d += 8 * U)
-        for (int u = 0; u < U; ++u) {
-          const __m256 kv = ld8<DT>(kp + (d + 8 * u) * elt);
-          for (int g = 0; g < G; ++g)
-            c[g][u] = _mm256_fmadd_ps(_mm256_loadu_ps(qf + g * D + d + 8 * u), kv, c[g][u]);
-        }
-      for (; d < D8; d += 8) {
-        const __m256 kv = ld8<DT>(kp + d * elt);
-        for (int g = 0; g < G; ++g)
-          c[g][0] = _mm256_fmadd_ps(_mm256_loadu_ps(qf + g * D + d), kv, c[g][0]);
-      }
-      for (int g = 0; g < G; ++g) {
-        __m256 sum = c[g][0];
-        for (int u = 1; u < U; ++u) sum = _mm256_add_ps(sum, c[g][u]);
-        float sc = hsum(sum);
-        for (int e = D8; e < D; ++e) sc += qf[g * D + e] * load1(kp, e, DT);
-        s[g * BS + t] = sc;
-      }
-    }
-    // one online-softmax step per head
-    for (int g = 0; g < G; ++g) {
-      float* sg = s + g * BS;
-      float bmax = sg[0];
-      for (int t = 1; t < ntok; ++t) bmax = std::max(bmax, sg[t]);
-      const float mn = std::max(m[g], bmax);
-      alpha[g] = m[g] == -INFINITY ? 0.f : exp2_1(m[g] - mn);
-      const __m256 mv = _mm256_set1_ps(mn);
-      __m256 ps = _mm256_setzero_ps();
-      int t = 0;
-      for (; t + 8 <= ntok; t += 8) {
-        const __m256 p = exp2_ps(_mm256_sub_ps(_mm256_loadu_ps(sg + t), mv));
-        _mm256_storeu_ps(sg + t, p);
-        ps = _mm256_add_ps(ps, p);
-      }
-      float psum = hsum(ps);
-      for (; t < ntok; ++t) {
-        sg[t] = exp2_1(sg[t] - mn);
-        psum += sg[t];
-      }
-      l[g] = l[g] * alpha[g] + psum;
-      m[g] = mn;
-    }
-    // acc = acc * alpha + P.V
-    const char* vb = vbase + base * elt;
-    int d = 0;
-    for (; d + 8 * CU <= D8; d += 8 * CU) {
-      __m256 r[G][CU];
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < CU; ++u)
-          r[g][u] = _mm256_mul_ps(_mm256_loadu_ps(acc + g * D + d + 8 * u), _mm256_set1_ps(alpha[g]));
-      for (int t = 0; t < ntok; ++t) {
-        const char* vp = vb + (int64_t)t * a.st * elt;
-        for (int u = 0; u < CU; ++u) {
-          const __m256 vv = ld8<DT>(vp + (d + 8 * u) * elt);
-          for (int g = 0; g < G; ++g)
-            r[g][u] = _mm256_fmadd_ps(_mm256_broadcast_ss(s + g * BS + t), vv, r[g][u]);
-        }
-      }
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < CU; ++u) _mm256_storeu_ps(acc + g * D + d + 8 * u, r[g][u]);
-    }
-    for (; d < D8; d += 8) {
-      __m256 r[G];
-      for (int g = 0; g < G; ++g)
-        r[g] = _mm256_mul_ps(_mm256_loadu_ps(acc + g * D + d), _mm256_set1_ps(alpha[g]));
-      for (int t = 0; t < ntok; ++t) {
-        const __m256 vv = ld8<DT>(vb + ((int64_t)t * a.st + d) * elt);
-        for (int g = 0; g < G; ++g)
-          r[g] = _mm256_fmadd_ps(_mm256_broadcast_ss(s + g * BS + t), vv, r[g]);
-      }
-      for (int g = 0; g < G; ++g) _mm256_storeu_ps(acc + g * D + d, r[g]);
-    }
-    for (; d < D; ++d)
-      for (int g = 0; g < G; ++g) {
-        float x = acc[g * D + d] * alpha[g];
-        for (int t = 0; t < ntok; ++t) x += s[g * BS + t] * load1(vb, (int64_t)t * a.st + d, DT);
-        acc[g * D + d] = x;
-      }
-  }
-  for (int g = 0; g < G; ++g) {
-    const int h = kh * Gr + g0 + g;
-    const float inv = 1.f / l[g];
-    float* o = acc + g * D;
-    for (int d = 0; d < D; ++d) o[d] *= inv;
-    const int64_t ob = (int64_t)i * a.out_ss + (int64_t)h * a.out_sh;
-    if (a.out_dt == FD_F32) {
-      memcpy(static_cast<float*>(a.out) + ob, o, (size_t)D * 4);
-    } else if (a.out_dt == FD_F16) {
-      uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
-      int d = 0;
-      for (; d + 8 <= D; d += 8)
-        _mm_storeu_si128(reinterpret_cast<__m128i*>(dst + d),
-                         _mm256_cvtps_ph(_mm256_loadu_ps(o + d), _MM_FROUND_TO_NEAREST_INT));
-      for (; d < D; ++d) dst[d] = _cvtss_sh(o[d], _MM_FROUND_TO_NEAREST_INT);
+  static float exp2_1(float x) { return _mm256_cvtss_f32(exp2(set1(x))); }
+  template <int DT>
+  static T ld(const void* p) {  // 8 storage elements -> fp32
+    if constexpr (DT == FD_F32) {
+      return _mm256_loadu_ps(static_cast<const float*>(p));
+    } else if constexpr (DT == FD_F16) {
+      return _mm256_cvtph_ps(_mm_loadu_si128(static_cast<const __m128i*>(p)));
     } else {
-      uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
-      for (int d = 0; d < D; ++d) dst[d] = f32_to_bf16(o[d]);
+      const __m256i w = _mm256_cvtepu16_epi32(_mm_loadu_si128(static_cast<const __m128i*>(p)));
+      return _mm256_castsi256_ps(_mm256_slli_epi32(w, 16));
     }
-    a.lse[(int64_t)h * a.lse_sh + i] = (m[g] + std::log2(l[g])) * 0.6931471805599453f;
   }
-  return true;
-}
+};
 
-template <int DT>
-bool run_heads_dt(const HostArgs& a, int i, int kh, int g0, int G, Scratch& w) {
-  switch (G) {
-    case 1: return run_heads<DT, 1>(a, i, kh, g0, w);
-    case 2: return run_heads<DT, 2>(a, i, kh, g0, w);
-    case 4: return run_heads<DT, 4>(a, i, kh, g0, w);
-    default: return run_heads<DT, 8>(a, i, kh, g0, w);
-  }
-}
+#include "host_decode_kernel.h"
 
+}  // namespace isa_avx2
 #pragma GCC pop_options
+
+// ---------------------------------------------------------------- AVX-512
+#pragma GCC push_options
+#pragma GCC target("avx512f,avx2,fma,f16c")
+namespace isa_avx512 {
+
+struct V {
+  using T = __m512;
+  static constexpr int W = 16;
+  static T zero() { return _mm512_setzero_ps(); }
+  static T set1(float x) { return _mm512_set1_ps(x); }
+  static T load(const float* p) { return _mm512_loadu_ps(p); }
+  static void store(float* p, T x) { _mm512_storeu_ps(p, x); }
+  static T bcast(const float* p) { return _mm512_set1_ps(*p); }
+  static T add(T a, T b) { return _mm512_add_ps(a, b); }
+  static T sub(T a, T b) { return _mm512_sub_ps(a, b); }
+  static T mul(T a, T b) { return _mm512_mul_ps(a, b); }
+  static T fma(T a, T b, T c) { return _mm512_fmadd_ps(a, b, c); }
+  static float hsum(T v) {
+    __m256 y = _mm256_add_ps(_mm512_castps512_ps256(v),
+                             _mm256_castpd_ps(_mm512_extractf64x4_pd(_mm512_castps_pd(v), 1)));
+    __m128 x = _mm_add_ps(_mm256_castps256_ps128(y), _mm256_extractf128_ps(y, 1));
+    x = _mm_add_ps(x, _mm_movehl_ps(x, x));
+    x = _mm_add_ss(x, _mm_shuffle_ps(x, x, 0x55));
+    return _mm_cvtss_f32(x);
+  }
+  static T exp2(T x) {
+    const T lo = set1(-126.f);
+    const __mmask16 keep = _mm512_cmp_ps_mask(x, lo, _CMP_NLT_UQ);  // not (x < -126)
+    x = _mm512_max_ps(lo, _mm512_min_ps(set1(127.f), x));
+    const T n = _mm512_roundscale_ps(x, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    const T f = sub(x, n);
+    const T p = FD_EXP2_POLY(fma, set1, f);
+    const __m512i e = _mm512_slli_epi32(_mm512_cvtps_epi32(n), 23);
+    return _mm512_maskz_mov_ps(keep,
+                               _mm512_castsi512_ps(_mm512_add_epi32(_mm512_castps_si512(p), e)));
+  }
+  static float exp2_1(float x) { return _mm512_cvtss_f32(exp2(set1(x))); }
+  template <int DT>
+  static T ld(const void* p) {  // 16 storage elements -> fp32
+    if constexpr (DT == FD_F32) {
+      return _mm512_loadu_ps(static_cast<const float*>(p));
+    } else if constexpr (DT == FD_F16) {
+      return _mm512_cvtph_ps(_mm256_loadu_si256(static_cast<const __m256i*>(p)));
+    } else {
+      const __m512i w = _mm512_cvtepu16_epi32(_mm256_loadu_si256(static_cast<const __m256i*>(p)));
+      return _mm512_castsi512_ps(_mm512_slli_epi32(w, 16));
+    }
+  }
+};
+
+#include "host_decode_kernel.h"
+
+}  // namespace isa_avx512
+#pragma GCC pop_options
+
+// Vector width the kernel uses on this CPU: 512 (AVX-512F) or 256 (AVX2),
+// 0 if neither is available. FASTDECODE_CPU_ISA=avx2 keeps to AVX2.
+int isa_bits() {
+  __builtin_cpu_init();
+  if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma") ||
+      !__builtin_cpu_supports("f16c"))
+    return 0;
+  const char* e = getenv("FASTDECODE_CPU_ISA");
+  if (e != nullptr && strcmp(e, "avx2") == 0) return 256;
+  return __builtin_cpu_supports("avx512f") ? 512 : 256;
+}
 
 // Fills every query head of kv head kh of sequence i with (x, lse); x is 0
 // or NaN.
@@ -410,20 +330,14 @@ void fill_item(const HostArgs& a, int i, int kh, float x, float lse) {
 }
 
 // All query heads of (sequence i, kv head kh), in passes of at most 8 heads.
-void run_item(const HostArgs& a, int i, int kh, Scratch& w) {
+void run_item(const HostArgs& a, int i, int kh, int bits, Scratch& w) {
   if (a.lens[i] <= 0) return fill_item(a, i, kh, 0.f, -INFINITY);
   const int Gr = a.H / a.KVH;
   for (int g0 = 0; g0 < Gr;) {
     const int rest = Gr - g0;
     const int G = rest >= 8 ? 8 : rest >= 4 ? 4 : rest >= 2 ? 2 : 1;
-    bool ok;
-    if (a.dt == FD_F16) {
-      ok = run_heads_dt<FD_F16>(a, i, kh, g0, G, w);
-    } else if (a.dt == FD_BF16) {
-      ok = run_heads_dt<FD_BF16>(a, i, kh, g0, G, w);
-    } else {
-      ok = run_heads_dt<FD_F32>(a, i, kh, g0, G, w);
-    }
+    const bool ok = bits == 512 ? isa_avx512::run_group(a, i, kh, g0, G, w)
+                                : isa_avx2::run_group(a, i, kh, g0, G, w);
     if (!ok) return fill_item(a, i, kh, NAN, NAN);
     g0 += G;
   }
@@ -443,6 +357,8 @@ int default_threads() {
 using namespace fd;
 
 extern "C" int fd_host_decode_threads(void) { return default_threads(); }
+
+extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 
 extern "C" int fd_host_decode_partial(
     const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
@@ -468,8 +384,8 @@ extern "C" int fd_host_decode_partial(
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: NULL pointer");
   if (bt_width > 0 && bt_stride < bt_width)
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: bt_stride < bt_width");
-  if (!__builtin_cpu_supports("avx2") || !__builtin_cpu_supports("fma") ||
-      !__builtin_cpu_supports("f16c"))
+  const int bits = isa_bits();
+  if (bits == 0)
     return set_error(FD_ERR_UNSUPPORTED, "fd_host_decode_partial: the CPU lacks AVX2/FMA/F16C");
   const HostArgs a{q, q_stride_seq, q_stride_head, k_cache, v_cache, kv_stride_block,
                    kv_stride_head, kv_stride_token, num_blocks, block_table, bt_stride, bt_width,
@@ -489,7 +405,7 @@ extern "C" int fd_host_decode_partial(
     for (;;) {
       const int64_t it = next.fetch_add(1, std::memory_order_relaxed);
       if (it >= items) break;
-      run_item(a, rows[it / num_kv_heads], (int)(it % num_kv_heads), w);
+      run_item(a, rows[it / num_kv_heads], (int)(it % num_kv_heads), bits, w);
     }
   });
   return FD_OK;

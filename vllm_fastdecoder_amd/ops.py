@@ -260,16 +260,19 @@ class HybridSplit:
     """A hybrid split decode in flight (hybrid_split_begin): the GPU's share
     is enqueued; finish() runs the host cores' share and enqueues the merge."""
 
-    def __init__(self, out, lse, o_gpu, l_gpu, q_host, q_ready, host_k_cache, host_v_cache,
-                 share, softmax_scale, num_threads):
+    def __init__(self, out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
+                 host_v_cache, share, softmax_scale, num_threads):
         self.out, self.lse = out, lse
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
-        self._q_host, self._q_ready = q_host, q_ready
+        self._q_host, self._q_ready, self._gpu_done = q_host, q_ready, gpu_done
         self._hk, self._hv = host_k_cache, host_v_cache
         self._share = share
         self._scale = softmax_scale
         self._threads = num_threads
         self.cpu_seconds = 0.0  # wall time of the host cores' share (0 before finish)
+        # whether the GPU's fused launch had completed when the host cores
+        # finished (None before finish): the signal that balances the share
+        self.gpu_finished_first: bool | None = None
 
     def finish(self) -> tuple[torch.Tensor, torch.Tensor]:
         """Waits for q on the host, reduces the host cores' blocks (blocking
@@ -288,9 +291,10 @@ class HybridSplit:
                          self._share.cpu_lens, self._scale, o_cpu, l_cpu,
                          num_threads=self._threads)
         self.cpu_seconds = time.perf_counter() - t0
+        self.gpu_finished_first = bool(self._gpu_done.query())
         merge_attn_states(self.out, self._o_gpu, self._l_gpu, o_cpu.to(dev, non_blocking=True),
                           l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
-        self._o_gpu = self._l_gpu = self._q_host = None
+        self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
         return self.out, self.lse
 
 
@@ -326,8 +330,8 @@ def hybrid_split_begin(
         lse = torch.empty(H, n, dtype=torch.float32, device=dev)
     share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
     if n == 0:
-        return HybridSplit(out, lse, None, None, None, None, host_k_cache, host_v_cache, share,
-                           softmax_scale, num_threads)
+        return HybridSplit(out, lse, None, None, None, None, None, host_k_cache, host_v_cache,
+                           share, softmax_scale, num_threads)
     q_host = torch.empty(q.shape, dtype=q.dtype, pin_memory=True)
     q_host.copy_(q, non_blocking=True)
     q_ready = torch.cuda.Event()
@@ -343,8 +347,10 @@ def hybrid_split_begin(
     split_decode(q, hbm_key_cache, hbm_value_cache, up(hbm_block_table), up(hbm_lens),
                  host_k_cache, host_v_cache, up(host_block_table), up(share.gpu_lens),
                  softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
-    return HybridSplit(out, lse, o_gpu, l_gpu, q_host, q_ready, host_k_cache, host_v_cache,
-                       share, softmax_scale, num_threads)
+    gpu_done = torch.cuda.Event()
+    gpu_done.record(torch.cuda.current_stream(dev))
+    return HybridSplit(out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
+                       host_v_cache, share, softmax_scale, num_threads)
 
 
 def hybrid_split_decode(

@@ -308,3 +308,27 @@ def share_host_blocks(host_bt: torch.Tensor, host_lens: torch.Tensor, block_size
     cpu_bt = (host_bt.gather(1, src) if W else torch.zeros(n, cols.numel(), dtype=torch.int32))
     cpu_bt = torch.where(cols[None, :] < k_cpu[:, None], cpu_bt, 0).to(torch.int32).contiguous()
     return HostShare(gpu_lens.to(torch.int32), cpu_bt, cpu_lens.to(torch.int32))
+
+
+class ShareTuner:
+    """Online balance of share_host_blocks' cpu_fraction between the host
+    cores and the GPU. After each hybrid step, `update(gpu_finished_first)`
+    moves the fraction one step toward the side that finished last: if the
+    GPU's launch was already complete when the host cores finished, the host
+    cores were the bottleneck and get less; otherwise more. The fraction
+    settles where both finish together and then alternates within one step of
+    it. No counterpart in the reference (its host cores take every host
+    block)."""
+
+    def __init__(self, start: float = 0.75, step: float = 0.01, lo: float = 0.05,
+                 hi: float = 1.0) -> None:
+        if not lo <= start <= hi:
+            raise ValueError("start must lie in [lo, hi]")
+        self.fraction = start
+        self.step = step
+        self.lo, self.hi = lo, hi
+
+    def update(self, gpu_finished_first: bool) -> float:
+        delta = -self.step if gpu_finished_first else self.step
+        self.fraction = min(self.hi, max(self.lo, self.fraction + delta))
+        return self.fraction
