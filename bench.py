@@ -465,7 +465,7 @@ def main() -> int:
     }
     del _keep, kc, vc
     torch.cuda.empty_cache()
-    if not args.no_split_run and w.name == "vicuna7b":
+    if not args.no_split_run and w.name in ("vicuna7b", "llama3_8b"):
         result["split_run"] = split_run(w, lens, bt, q, args.steps, args.warmup, stream)
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:

@@ -329,9 +329,11 @@ int fd_host_decode_partial(
 int fd_host_decode_threads(void);
 
 /* Vector width in bits fd_host_decode_partial uses on this CPU: 512
- * (AVX-512F), 256 (AVX2; also when FASTDECODE_CPU_ISA=avx2), 0 (neither:
- * the call fails with FD_ERR_UNSUPPORTED). No counterpart in the reference
- * (its kernel is compiled for one ISA, cpu_attn.cpp:1-40). */
+ * (AVX-512F; bf16 KV scores by vdpbf16ps where AVX512_BF16 is present,
+ * unless FASTDECODE_CPU_ISA=avx512), 256 (AVX2; also when
+ * FASTDECODE_CPU_ISA=avx2), 0 (neither: the call fails with
+ * FD_ERR_UNSUPPORTED). No counterpart in the reference (its kernel is
+ * compiled for one ISA, cpu_attn.cpp:1-40). */
 int fd_host_decode_isa(void);
 
 /* ------------------------------------------------------------------------

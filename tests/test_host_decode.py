@@ -27,15 +27,23 @@ from vllm_fastdecoder_amd import _lib, ops
 OUT_TOL_16BIT = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2, torch.float32: 1e-5}
 
 
-@pytest.fixture(params=["widest", "avx2"])
+@pytest.fixture(params=["widest", "avx512", "avx2"])
 def isa(request, monkeypatch):
-    """Each case on the widest vector ISA of this CPU and on the AVX2 body."""
+    """Each case on every kernel body this CPU runs: the widest (AVX-512 with
+    bf16 pair dot products where the CPU has them), plain AVX-512, AVX2."""
+    lib = _lib.load_lib()
+    monkeypatch.delenv("FASTDECODE_CPU_ISA", raising=False)
+    widest = lib.fd_host_decode_isa()
     if request.param == "avx2":
         monkeypatch.setenv("FASTDECODE_CPU_ISA", "avx2")
-        assert _lib.load_lib().fd_host_decode_isa() == 256
+        assert lib.fd_host_decode_isa() == 256
+    elif request.param == "avx512":
+        if widest != 512:
+            pytest.skip("no AVX-512 on this CPU")
+        monkeypatch.setenv("FASTDECODE_CPU_ISA", "avx512")
+        assert lib.fd_host_decode_isa() == 512
     else:
-        monkeypatch.delenv("FASTDECODE_CPU_ISA", raising=False)
-        assert _lib.load_lib().fd_host_decode_isa() in (256, 512)
+        assert widest in (256, 512)
     return request.param
 
 

@@ -21,9 +21,11 @@
 // bf16 rows, and exp2 from a degree-6 polynomial for 2^f on [-0.5, 0.5]
 // (least-squares fit on Chebyshev nodes, relative error < 1e-7 in fp32) times
 // 2^n assembled in the exponent field. One kernel body
-// (host_decode_kernel.h) is compiled for AVX-512 (16 lanes) and for AVX2 (8
-// lanes) and the widest one the CPU supports is picked at run time; the rest
-// of the library is built for baseline x86-64.
+// (host_decode_kernel.h) is compiled for AVX-512 with bf16 pair dot products
+// (bf16 KV scores by vdpbf16ps on the raw q and K rows, the scale applied to
+// the dot), plain AVX-512 (16 lanes) and AVX2 (8 lanes); the widest one the
+// CPU supports is picked at run time, and the rest of the library is built
+// for baseline x86-64.
 #include <immintrin.h>
 #include <sched.h>
 #include <stdint.h>
@@ -175,6 +177,7 @@ uint16_t f32_to_bf16(float x) {
 // Scratch of one worker.
 struct Scratch {
   std::vector<float> q, acc, s;
+  std::vector<uint16_t> qh;
 };
 
 constexpr int kPrefetchBlocks = 1;  // how far ahead the next block's rows are prefetched
@@ -199,6 +202,10 @@ namespace isa_avx2 {
 struct V {
   using T = __m256;
   static constexpr int W = 8;
+  static constexpr int kAcc = 8;  // P.V accumulators kept live (16 registers)
+  static constexpr bool kBf16Dot = false;
+  static __m256i ld_bf16x32(const void*) { return _mm256_setzero_si256(); }  // unused
+  static T dot_bf16(T c, __m256i, __m256i) { return c; }                     // unused
   static T zero() { return _mm256_setzero_ps(); }
   static T set1(float x) { return _mm256_set1_ps(x); }
   static T load(const float* p) { return _mm256_loadu_ps(p); }
@@ -248,9 +255,13 @@ struct V {
 #pragma GCC target("avx512f,avx2,fma,f16c")
 namespace isa_avx512 {
 
-struct V {
+struct V512 {
   using T = __m512;
   static constexpr int W = 16;
+  static constexpr int kAcc = 16;  // P.V accumulators kept live (32 registers)
+  static constexpr bool kBf16Dot = false;
+  static __m512i ld_bf16x32(const void*) { return _mm512_setzero_si512(); }  // unused
+  static T dot_bf16(T c, __m512i, __m512i) { return c; }                     // unused
   static T zero() { return _mm512_setzero_ps(); }
   static T set1(float x) { return _mm512_set1_ps(x); }
   static T load(const float* p) { return _mm512_loadu_ps(p); }
@@ -293,9 +304,29 @@ struct V {
   }
 };
 
+using V = V512;
+
 #include "host_decode_kernel.h"
 
 }  // namespace isa_avx512
+#pragma GCC pop_options
+
+// ------------------------------------------------ AVX-512 with BF16 dot products
+#pragma GCC push_options
+#pragma GCC target("avx512f,avx512bf16,avx2,fma,f16c")
+namespace isa_avx512bf16 {
+
+struct V : isa_avx512::V512 {
+  static constexpr bool kBf16Dot = true;  // scores of bf16 KV by vdpbf16ps
+  static __m512bh ld_bf16x32(const void* p) {
+    return (__m512bh)_mm512_loadu_si512(p);
+  }
+  static T dot_bf16(T c, __m512bh a, __m512bh b) { return _mm512_dpbf16_ps(c, a, b); }
+};
+
+#include "host_decode_kernel.h"
+
+}  // namespace isa_avx512bf16
 #pragma GCC pop_options
 
 // Vector width the kernel uses on this CPU: 512 (AVX-512F) or 256 (AVX2),
@@ -308,6 +339,14 @@ int isa_bits() {
   const char* e = getenv("FASTDECODE_CPU_ISA");
   if (e != nullptr && strcmp(e, "avx2") == 0) return 256;
   return __builtin_cpu_supports("avx512f") ? 512 : 256;
+}
+
+// The AVX-512 body with bf16 pair dot products, where the CPU has them
+// (FASTDECODE_CPU_ISA=avx512 keeps to plain AVX-512).
+bool use_bf16_dot() {
+  const char* e = getenv("FASTDECODE_CPU_ISA");
+  if (e != nullptr && strcmp(e, "avx512") == 0) return false;
+  return __builtin_cpu_supports("avx512bf16");
 }
 
 // Fills every query head of kv head kh of sequence i with (x, lse); x is 0
@@ -336,8 +375,9 @@ void run_item(const HostArgs& a, int i, int kh, int bits, Scratch& w) {
   for (int g0 = 0; g0 < Gr;) {
     const int rest = Gr - g0;
     const int G = rest >= 8 ? 8 : rest >= 4 ? 4 : rest >= 2 ? 2 : 1;
-    const bool ok = bits == 512 ? isa_avx512::run_group(a, i, kh, g0, G, w)
-                                : isa_avx2::run_group(a, i, kh, g0, G, w);
+    const bool ok = bits == 513   ? isa_avx512bf16::run_group(a, i, kh, g0, G, w)
+                    : bits == 512 ? isa_avx512::run_group(a, i, kh, g0, G, w)
+                                  : isa_avx2::run_group(a, i, kh, g0, G, w);
     if (!ok) return fill_item(a, i, kh, NAN, NAN);
     g0 += G;
   }
@@ -384,9 +424,10 @@ extern "C" int fd_host_decode_partial(
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: NULL pointer");
   if (bt_width > 0 && bt_stride < bt_width)
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: bt_stride < bt_width");
-  const int bits = isa_bits();
+  int bits = isa_bits();
   if (bits == 0)
     return set_error(FD_ERR_UNSUPPORTED, "fd_host_decode_partial: the CPU lacks AVX2/FMA/F16C");
+  if (bits == 512 && use_bf16_dot()) bits = 513;  // internal tag of the bf16-dot body
   const HostArgs a{q, q_stride_seq, q_stride_head, k_cache, v_cache, kv_stride_block,
                    kv_stride_head, kv_stride_token, num_blocks, block_table, bt_stride, bt_width,
                    lens, n, num_heads, num_kv_heads, head_size, block_size, scale, kv_dtype, out,

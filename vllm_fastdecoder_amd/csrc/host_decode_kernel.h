@@ -8,6 +8,106 @@
 // Needs, from the including namespace: V, HostArgs, Scratch, load1,
 // f32_to_bf16, kPrefetchBlocks.
 
+// acc[g][d0 .. d0 + W*CU) = acc * alpha[g] + sum_t s[g][t] * V[t][...] for as
+// many whole groups of CU chunks as fit below DW, advancing d; the rest goes
+// to groups of CU / 2, and so on. The G*CU accumulators stay in registers.
+template <int DT, int G, int CU>
+__attribute__((always_inline)) inline void pv_groups(float* acc, const float* s, const float* alpha, const char* vb,
+                      int64_t st, int D, int DW, int BS, int ntok, int& d) {
+  using T = typename V::T;
+  constexpr int W = V::W;
+  constexpr int elt = DT == FD_F32 ? 4 : 2;
+  for (; d + W * CU <= DW; d += W * CU) {
+    T r[G][CU];
+    for (int g = 0; g < G; ++g)
+      for (int u = 0; u < CU; ++u)
+        r[g][u] = V::mul(V::load(acc + g * D + d + W * u), V::set1(alpha[g]));
+    for (int t = 0; t < ntok; ++t) {
+      const char* vp = vb + (int64_t)t * st * elt;
+      T p[G];
+      for (int g = 0; g < G; ++g) p[g] = V::bcast(s + g * BS + t);
+      for (int u = 0; u < CU; ++u) {
+        const T vv = V::template ld<DT>(vp + (d + W * u) * elt);
+        for (int g = 0; g < G; ++g) r[g][u] = V::fma(p[g], vv, r[g][u]);
+      }
+    }
+    for (int g = 0; g < G; ++g)
+      for (int u = 0; u < CU; ++u) V::store(acc + g * D + d + W * u, r[g][u]);
+  }
+  if constexpr (CU > 1) pv_groups<DT, G, CU / 2>(acc, s, alpha, vb, st, D, DW, BS, ntok, d);
+}
+
+// s[g * BS] = q[g] . K row at kp for the G heads, with U independent
+// accumulator chains per head; every loop over heads and chains is unrolled so
+// the G*U accumulators stay in registers.
+template <int DT, int G, int U>
+__attribute__((always_inline)) inline void score_token(const char* kp, const float* qf,
+                                                       const uint16_t* qh, float qs, int D, int DW,
+                                                       float* s, int BS) {
+  using T = typename V::T;
+  constexpr int W = V::W;
+  constexpr int elt = DT == FD_F32 ? 4 : 2;
+  if constexpr (V::kBf16Dot && DT == FD_BF16) {
+    if (D % 32 == 0) {  // bf16 pair dot products on the raw q and K rows
+      constexpr int UB = U > 4 ? 4 : U;
+      T c[G][UB];
+#pragma GCC unroll 64
+      for (int j = 0; j < G * UB; ++j) c[j / UB][j % UB] = V::zero();
+      int d = 0;
+      for (; d + 32 * UB <= D; d += 32 * UB) {
+#pragma GCC unroll 16
+        for (int u = 0; u < UB; ++u) {
+          const auto kv = V::ld_bf16x32(kp + (d + 32 * u) * 2);
+#pragma GCC unroll 16
+          for (int g = 0; g < G; ++g) c[g][u] = V::dot_bf16(c[g][u], V::ld_bf16x32(qh + g * D + d + 32 * u), kv);
+        }
+      }
+      for (; d < D; d += 32) {
+        const auto kv = V::ld_bf16x32(kp + d * 2);
+#pragma GCC unroll 16
+        for (int g = 0; g < G; ++g) c[g][0] = V::dot_bf16(c[g][0], V::ld_bf16x32(qh + g * D + d), kv);
+      }
+#pragma GCC unroll 16
+      for (int g = 0; g < G; ++g) {
+#pragma GCC unroll 16
+        for (int step = 1; step < UB; step *= 2)
+#pragma GCC unroll 16
+          for (int u = 0; u + step < UB; u += 2 * step) c[g][u] = V::add(c[g][u], c[g][u + step]);
+        s[g * BS] = V::hsum(c[g][0]) * qs;
+      }
+      return;
+    }
+  }
+  T c[G][U];
+#pragma GCC unroll 64
+  for (int j = 0; j < G * U; ++j) c[j / U][j % U] = V::zero();
+  int d = 0;
+  for (; d + W * U <= DW; d += W * U) {
+#pragma GCC unroll 16
+    for (int u = 0; u < U; ++u) {
+      const T kv = V::template ld<DT>(kp + (d + W * u) * elt);
+#pragma GCC unroll 16
+      for (int g = 0; g < G; ++g)
+        c[g][u] = V::fma(V::load(qf + g * D + d + W * u), kv, c[g][u]);
+    }
+  }
+  for (; d < DW; d += W) {
+    const T kv = V::template ld<DT>(kp + d * elt);
+#pragma GCC unroll 16
+    for (int g = 0; g < G; ++g) c[g][0] = V::fma(V::load(qf + g * D + d), kv, c[g][0]);
+  }
+#pragma GCC unroll 16
+  for (int g = 0; g < G; ++g) {
+#pragma GCC unroll 16
+    for (int step = 1; step < U; step *= 2)  // pairwise sum of the chains
+#pragma GCC unroll 16
+      for (int u = 0; u + step < U; u += 2 * step) c[g][u] = V::add(c[g][u], c[g][u + step]);
+    float sc = V::hsum(c[g][0]);
+    for (int e = DW; e < D; ++e) sc += qf[g * D + e] * load1(kp, e, DT);
+    s[g * BS] = sc;
+  }
+}
+
 // Online-softmax partial of query heads kh*Gr + g0 .. + G-1 (Gr = H / KVH) of
 // sequence i over kv head kh. Returns false if the row is invalid (a length
 // past its table or a block id outside the cache).
@@ -16,8 +116,8 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
   using T = typename V::T;
   constexpr int W = V::W;
   constexpr int elt = DT == FD_F32 ? 4 : 2;
-  constexpr int U = G >= 4 ? 1 : 4 / G;   // score chains per head
-  constexpr int CU = G >= 8 ? 1 : 8 / G;  // P.V chunks in flight
+  constexpr int U = G >= 8 ? 1 : 8 / G;   // score chains per head (>= 8 in all)
+  constexpr int CU = G >= V::kAcc ? 1 : V::kAcc / G;  // P.V chunks in flight
   const int D = a.D, BS = a.BS, Gr = a.H / a.KVH;
   const int DW = D - D % W;
   const int L = a.lens[i];
@@ -33,6 +133,15 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
   for (int g = 0; g < G; ++g) {
     const int64_t qb = (int64_t)i * a.q_ss + (int64_t)(kh * Gr + g0 + g) * a.q_sh;
     for (int d = 0; d < D; ++d) qf[g * D + d] = load1(a.q, qb + d, a.dt) * qs;
+  }
+  const uint16_t* qh = nullptr;  // the raw bf16 q rows, for the pair dot products
+  if constexpr (V::kBf16Dot && DT == FD_BF16) {
+    w.qh.resize((size_t)G * D);
+    for (int g = 0; g < G; ++g) {
+      const int64_t qb = (int64_t)i * a.q_ss + (int64_t)(kh * Gr + g0 + g) * a.q_sh;
+      memcpy(w.qh.data() + (size_t)g * D, static_cast<const uint16_t*>(a.q) + qb, (size_t)D * 2);
+    }
+    qh = w.qh.data();
   }
   float m[G], l[G], alpha[G];
   for (int g = 0; g < G; ++g) {
@@ -59,30 +168,9 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
       }
     }
     // scores
-    for (int t = 0; t < ntok; ++t) {
-      const char* kp = kbase + (base + (int64_t)t * a.st) * elt;
-      T c[G][U];
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < U; ++u) c[g][u] = V::zero();
-      int d = 0;
-      for (; d + W * U <= DW; d += W * U)
-        for (int u = 0; u < U; ++u) {
-          const T kv = V::template ld<DT>(kp + (d + W * u) * elt);
-          for (int g = 0; g < G; ++g)
-            c[g][u] = V::fma(V::load(qf + g * D + d + W * u), kv, c[g][u]);
-        }
-      for (; d < DW; d += W) {
-        const T kv = V::template ld<DT>(kp + d * elt);
-        for (int g = 0; g < G; ++g) c[g][0] = V::fma(V::load(qf + g * D + d), kv, c[g][0]);
-      }
-      for (int g = 0; g < G; ++g) {
-        T sum = c[g][0];
-        for (int u = 1; u < U; ++u) sum = V::add(sum, c[g][u]);
-        float sc = V::hsum(sum);
-        for (int e = DW; e < D; ++e) sc += qf[g * D + e] * load1(kp, e, DT);
-        s[g * BS + t] = sc;
-      }
-    }
+    for (int t = 0; t < ntok; ++t)
+      score_token<DT, G, U>(kbase + (base + (int64_t)t * a.st) * elt, qf, qh, qs, D, DW, s + t,
+                            BS);
     // one online-softmax step per head
     for (int g = 0; g < G; ++g) {
       float* sg = s + g * BS;
@@ -106,33 +194,11 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
       l[g] = l[g] * alpha[g] + psum;
       m[g] = mn;
     }
-    // acc = acc * alpha + P.V
+    // acc = acc * alpha + P.V, CU chunks of W columns at a time, then
+    // halving groups for what is left
     const char* vb = vbase + base * elt;
     int d = 0;
-    for (; d + W * CU <= DW; d += W * CU) {
-      T r[G][CU];
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < CU; ++u)
-          r[g][u] = V::mul(V::load(acc + g * D + d + W * u), V::set1(alpha[g]));
-      for (int t = 0; t < ntok; ++t) {
-        const char* vp = vb + (int64_t)t * a.st * elt;
-        for (int u = 0; u < CU; ++u) {
-          const T vv = V::template ld<DT>(vp + (d + W * u) * elt);
-          for (int g = 0; g < G; ++g) r[g][u] = V::fma(V::bcast(s + g * BS + t), vv, r[g][u]);
-        }
-      }
-      for (int g = 0; g < G; ++g)
-        for (int u = 0; u < CU; ++u) V::store(acc + g * D + d + W * u, r[g][u]);
-    }
-    for (; d < DW; d += W) {
-      T r[G];
-      for (int g = 0; g < G; ++g) r[g] = V::mul(V::load(acc + g * D + d), V::set1(alpha[g]));
-      for (int t = 0; t < ntok; ++t) {
-        const T vv = V::template ld<DT>(vb + ((int64_t)t * a.st + d) * elt);
-        for (int g = 0; g < G; ++g) r[g] = V::fma(V::bcast(s + g * BS + t), vv, r[g]);
-      }
-      for (int g = 0; g < G; ++g) V::store(acc + g * D + d, r[g]);
-    }
+    pv_groups<DT, G, CU>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
     for (; d < D; ++d)
       for (int g = 0; g < G; ++g) {
         float x = acc[g * D + d] * alpha[g];
