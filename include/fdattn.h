@@ -324,9 +324,31 @@ int fd_host_decode_partial(
     float* lse, int64_t lse_stride_head,
     int32_t num_threads);
 
-/* Worker count fd_host_decode_partial uses when num_threads is 0. No
- * counterpart in the reference (it uses OpenMP's default team). */
+/* Worker count fd_host_decode_partial uses when num_threads is 0: the count
+ * set by fd_host_set_threads, else FASTDECODE_CPU_THREADS, else one per CPU
+ * of the process's affinity mask. Replaces the extension's get_num_threads
+ * (cpu_attn.cpp:36-40,523). */
 int fd_host_decode_threads(void);
+
+/* Sets that count for the process (n <= 0 restores the default). Replaces
+ * the extension's set_num_threads (cpu_attn.cpp:521). */
+int fd_host_set_threads(int32_t n);
+
+/* Host-tier slot write on the host cores: the reference's store_kv
+ * (cpu_attn.cpp:491-517, body :413-431) with host pointers.
+ *   cache[slot / BS][kv head][slot % BS][:] = k[j][kv head][:]  (and V)
+ * for j < m. k, v [m, KVH, D] with strides (k_stride_tok, k_stride_head, 1);
+ * caches [num_blocks, KVH, BS, D] of dtype with strides (block, head, token).
+ * Every slot is checked against [0, num_blocks * block_size) before any
+ * write: FD_ERR_RANGE ("CPU slot out of range") and nothing written
+ * otherwise. Synchronous; bit-exact copies. */
+int fd_host_store_kv(const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                     const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                     void* k_cache, void* v_cache, int64_t cache_stride_block,
+                     int64_t cache_stride_head, int64_t cache_stride_token,
+                     int64_t num_blocks, const int64_t* slots, int64_t m,
+                     int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                     int32_t dtype);
 
 /* Vector width in bits fd_host_decode_partial uses on this CPU: 512
  * (AVX-512F; bf16 KV scores by vdpbf16ps where AVX512_BF16 is present,

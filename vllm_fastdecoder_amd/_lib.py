@@ -140,6 +140,19 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "fd_host_decode_threads": (c_int, []),
     "fd_host_decode_isa": (c_int, []),
+    "fd_host_set_threads": (c_int, [c_int32]),
+    "fd_host_store_kv": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int64,            # k, strides token/head
+            c_void_p, c_int64, c_int64,            # v, strides token/head
+            c_void_p, c_void_p,                    # k_cache, v_cache
+            c_int64, c_int64, c_int64,             # cache strides block/head/token
+            c_int64,                               # num_blocks
+            c_void_p, c_int64,                     # slots, m
+            c_int32, c_int32, c_int32, c_int32,    # KVH, D, BS, dtype
+        ],
+    ),
     "fd_stream_copy": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
 }
 

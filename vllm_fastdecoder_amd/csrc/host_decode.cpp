@@ -383,7 +383,11 @@ void run_item(const HostArgs& a, int i, int kh, int bits, Scratch& w) {
   }
 }
 
+std::atomic<int> g_threads{0};  // set by fd_host_set_threads; 0 = the default below
+
 int default_threads() {
+  const int set_n = g_threads.load(std::memory_order_relaxed);
+  if (set_n > 0) return set_n;
   const char* e = getenv("FASTDECODE_CPU_THREADS");
   if (e != nullptr && atoi(e) > 0) return atoi(e);
   cpu_set_t set;
@@ -397,6 +401,43 @@ int default_threads() {
 using namespace fd;
 
 extern "C" int fd_host_decode_threads(void) { return default_threads(); }
+
+extern "C" int fd_host_set_threads(int32_t n) {
+  g_threads.store(n > 0 ? n : 0, std::memory_order_relaxed);
+  return FD_OK;
+}
+
+extern "C" int fd_host_store_kv(const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                void* k_cache, void* v_cache, int64_t cache_stride_block,
+                                int64_t cache_stride_head, int64_t cache_stride_token,
+                                int64_t num_blocks, const int64_t* slots, int64_t m,
+                                int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                                int32_t dtype) {
+  if (m < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 || num_blocks < 0)
+    return set_error(FD_ERR_INVALID, "fd_host_store_kv: bad sizes");
+  if (dtype != FD_F16 && dtype != FD_BF16 && dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "fd_host_store_kv: unsupported dtype %d", dtype);
+  if (m == 0) return FD_OK;
+  if (!k || !v || !k_cache || !v_cache || !slots)
+    return set_error(FD_ERR_INVALID, "fd_host_store_kv: NULL pointer");
+  const int64_t capacity = num_blocks * block_size;
+  for (int64_t j = 0; j < m; ++j)  // every slot before any write
+    if (slots[j] < 0 || slots[j] >= capacity)
+      return set_error(FD_ERR_RANGE, "CPU slot out of range: %lld", (long long)slots[j]);
+  const size_t elt = dtype == FD_F32 ? 4 : 2, row = elt * (size_t)head_size;
+  for (int64_t j = 0; j < m; ++j) {
+    const int64_t blk = slots[j] / block_size, off = slots[j] % block_size;
+    for (int kh = 0; kh < num_kv_heads; ++kh) {
+      const int64_t dst = blk * cache_stride_block + kh * cache_stride_head + off * cache_stride_token;
+      memcpy(static_cast<char*>(k_cache) + dst * elt,
+             static_cast<const char*>(k) + (j * k_stride_tok + kh * k_stride_head) * elt, row);
+      memcpy(static_cast<char*>(v_cache) + dst * elt,
+             static_cast<const char*>(v) + (j * v_stride_tok + kh * v_stride_head) * elt, row);
+    }
+  }
+  return FD_OK;
+}
 
 extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 
