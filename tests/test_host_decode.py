@@ -201,3 +201,33 @@ def test_host_decode_rejects_bad_arguments():
     assert lib.fd_host_decode_partial(None, 0, 0, None, None, 0, 0, 0, 0, None, 0, 0, None, 0, 4,
                                       2, 64, 16, 0.1, _lib.FD_F16, None, 0, 0, _lib.FD_F16,
                                       None, 0, 0) == _lib.FD_OK
+
+
+def _child_decode(conn, args):
+    q, kc, vc, bt, lens = args
+    out, lse = run(q, kc, vc, bt, lens, 0.1, torch.float32, threads=4)
+    conn.send((out.numpy().copy(), lse.numpy().copy()))  # by value, not shared memory
+    conn.close()
+
+
+def test_host_decode_in_a_forked_child():
+    """A child forked after the parent used the worker pool gets its own pool
+    (the parent's threads do not exist in the child): same results, no hang."""
+    import multiprocessing as mp
+
+    args = cases.rand_case(11, 8, 2, 64, 16, 60, torch.float16, 150, 3)
+    parent = run(*args[:5], 0.1, torch.float32, threads=4)
+    ctx = mp.get_context("fork")
+    rd, wr = ctx.Pipe(duplex=False)
+    proc = ctx.Process(target=_child_decode, args=(wr, args))
+    proc.start()
+    wr.close()
+    try:
+        assert rd.poll(120), "forked child did not answer"
+        child = tuple(torch.from_numpy(x) for x in rd.recv())
+    finally:
+        proc.join(30)
+        if proc.is_alive():
+            proc.kill()
+    assert proc.exitcode == 0
+    assert torch.equal(child[0], parent[0]) and torch.equal(child[1], parent[1])

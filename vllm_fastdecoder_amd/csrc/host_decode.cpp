@@ -28,6 +28,7 @@
 // for baseline x86-64.
 #include <immintrin.h>
 #include <sched.h>
+#include <unistd.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -109,12 +110,31 @@ class Pool {
   bool stop_ = false;
 };
 
-Pool& pool() {
-  static Pool p;
-  return p;
-}
+// The pool and the lock that serialises calls on it, per process: a child
+// forked from a process that used them gets new ones (the parent's worker
+// threads do not exist in the child, and the lock may have been held at the
+// fork). The parent's objects are left alone in the child, never destroyed.
+struct PoolState {
+  pid_t pid;
+  Pool pool;
+  std::mutex call_mu;
+  explicit PoolState(pid_t p) : pid(p) {}
+};
 
-std::mutex g_call_mu;  // the pool serves one call at a time
+PoolState& pool_state() {
+  static std::atomic<PoolState*> state{nullptr};
+  static std::mutex create_mu;  // taken only to create the state of a process
+  const pid_t me = getpid();
+  PoolState* st = state.load(std::memory_order_acquire);
+  if (st != nullptr && st->pid == me) return *st;
+  std::lock_guard<std::mutex> lk(create_mu);
+  st = state.load(std::memory_order_acquire);
+  if (st == nullptr || st->pid != me) {
+    st = new PoolState(me);  // intentionally never freed (lives for the process)
+    state.store(st, std::memory_order_release);
+  }
+  return *st;
+}
 
 struct HostArgs {
   const void* q;
@@ -481,8 +501,9 @@ extern "C" int fd_host_decode_partial(
   const int nt = (int)std::max<int64_t>(
       1, std::min<int64_t>(num_threads > 0 ? num_threads : default_threads(), items));
   std::atomic<int64_t> next{0};
-  std::lock_guard<std::mutex> call(g_call_mu);
-  pool().run(nt, [&](int) {
+  PoolState& ps = pool_state();
+  std::lock_guard<std::mutex> call(ps.call_mu);
+  ps.pool.run(nt, [&](int) {
     Scratch w;
     for (;;) {
       const int64_t it = next.fetch_add(1, std::memory_order_relaxed);
