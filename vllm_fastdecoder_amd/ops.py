@@ -18,6 +18,7 @@ from __future__ import annotations
 import ctypes
 import threading
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -256,13 +257,75 @@ def split_decode(
     return out, lse
 
 
+class _HybridStaging:
+    """Grow-only pinned host buffers of the hybrid split, one set per device
+    (the grow-only policy of the reference's PinnedStaging, state.py:93-124):
+    q on its way to the host cores, their fp32 partial on its way back, and
+    the host-planned index tensors on their way to the GPU. Reused every
+    step, so a step allocates no pinned memory. One hybrid step may be in
+    flight per device; the next one waits (usually not at all) until the
+    previous step's copies out of the buffers have completed."""
+
+    def __init__(self) -> None:
+        self._bufs: dict[tuple[int, str], torch.Tensor] = {}
+        self._released: dict[int, torch.cuda.Event] = {}
+        self._pending: set[int] = set()
+        self._lock = threading.Lock()
+
+    def acquire(self, dev: torch.device) -> int:
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        with self._lock:
+            if idx in self._pending:
+                raise RuntimeError("a hybrid split is already in flight on this device; "
+                                   "finish() it before starting another")
+            self._pending.add(idx)
+            ev = self._released.get(idx)
+        if ev is not None:
+            ev.synchronize()
+        return idx
+
+    def release(self, idx: int, stream) -> None:
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        with self._lock:
+            self._released[idx] = ev
+            self._pending.discard(idx)
+
+    def view(self, idx: int, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
+        numel = 1
+        for d in shape:
+            numel *= int(d)
+        nbytes = max(numel * torch.empty(0, dtype=dtype).element_size(), 1)
+        with self._lock:
+            buf = self._bufs.get((idx, name))
+            if buf is None or buf.numel() < nbytes:
+                cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
+                buf = torch.empty(cap, dtype=torch.uint8, pin_memory=True)
+                self._bufs[(idx, name)] = buf
+        return buf[:numel * torch.empty(0, dtype=dtype).element_size()].view(dtype).view(shape)
+
+    def upload(self, idx: int, name: str, t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+        """A host tensor copied to the device through its pinned buffer (the
+        host-side copy by numpy: single-threaded, leaving no spinning OpenMP
+        team behind on the host cores)."""
+        if t.is_cuda:
+            return t
+        v = self.view(idx, name, t.shape, t.dtype)
+        np.copyto(v.numpy(), t.numpy())
+        return v.to(dev, non_blocking=True)
+
+
+HYBRID_STAGING = _HybridStaging()
+
+
 class HybridSplit:
     """A hybrid split decode in flight (hybrid_split_begin): the GPU's share
     is enqueued; finish() runs the host cores' share and enqueues the merge."""
 
     def __init__(self, out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
-                 host_v_cache, share, softmax_scale, num_threads):
+                 host_v_cache, share, softmax_scale, num_threads, staging_idx=None):
         self.out, self.lse = out, lse
+        self._staging_idx = staging_idx
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
         self._q_host, self._q_ready, self._gpu_done = q_host, q_ready, gpu_done
         self._hk, self._hv = host_k_cache, host_v_cache
@@ -283,18 +346,23 @@ class HybridSplit:
 
         dev = self.out.device
         n, H, D = self.out.shape
-        o_cpu = torch.empty(n, H, D, dtype=torch.float32, pin_memory=True)
-        l_cpu = torch.empty(H, n, dtype=torch.float32, pin_memory=True)
-        self._q_ready.synchronize()
-        t0 = time.perf_counter()
-        host_decode_attn(self._q_host, self._hk, self._hv, self._share.cpu_bt,
-                         self._share.cpu_lens, self._scale, o_cpu, l_cpu,
-                         num_threads=self._threads)
-        self.cpu_seconds = time.perf_counter() - t0
-        self.gpu_finished_first = bool(self._gpu_done.query())
-        merge_attn_states(self.out, self._o_gpu, self._l_gpu, o_cpu.to(dev, non_blocking=True),
-                          l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
-        self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
+        idx = self._staging_idx
+        try:
+            o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
+            l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
+            self._q_ready.synchronize()
+            t0 = time.perf_counter()
+            host_decode_attn(self._q_host, self._hk, self._hv, self._share.cpu_bt,
+                             self._share.cpu_lens, self._scale, o_cpu, l_cpu,
+                             num_threads=self._threads)
+            self.cpu_seconds = time.perf_counter() - t0
+            self.gpu_finished_first = bool(self._gpu_done.query())
+            merge_attn_states(self.out, self._o_gpu, self._l_gpu,
+                              o_cpu.to(dev, non_blocking=True), l_cpu.to(dev, non_blocking=True),
+                              out_lse=self.lse)
+        finally:
+            HYBRID_STAGING.release(idx, torch.cuda.current_stream(dev))
+            self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
         return self.out, self.lse
 
 
@@ -332,25 +400,36 @@ def hybrid_split_begin(
     if n == 0:
         return HybridSplit(out, lse, None, None, None, None, None, host_k_cache, host_v_cache,
                            share, softmax_scale, num_threads)
-    q_host = torch.empty(q.shape, dtype=q.dtype, pin_memory=True)
-    q_host.copy_(q, non_blocking=True)
-    q_ready = torch.cuda.Event()
-    q_ready.record(torch.cuda.current_stream(dev))
+    stream = torch.cuda.current_stream(dev)
+    idx = HYBRID_STAGING.acquire(dev)
+    try:
+        q_host = HYBRID_STAGING.view(idx, "q", q.shape, q.dtype)
+        q_host.copy_(q, non_blocking=True)
+        q_ready = torch.cuda.Event()
+        q_ready.record(stream)
 
-    def up(t):  # host index tensors: pinned, asynchronous upload
-        return t if t.is_cuda else t.pin_memory().to(dev, non_blocking=True)
+        def up(name, t):  # host index tensors: through pinned staging, asynchronous
+            return HYBRID_STAGING.upload(idx, name, t, dev)
 
-    # rows by decreasing GPU work when the HBM lengths are known on the host
-    order = None if hbm_lens.is_cuda else up(_longest_first(hbm_lens + share.gpu_lens))
-    o_gpu = torch.empty(n, H, D, dtype=torch.float32, device=dev)
-    l_gpu = torch.empty(H, n, dtype=torch.float32, device=dev)
-    split_decode(q, hbm_key_cache, hbm_value_cache, up(hbm_block_table), up(hbm_lens),
-                 host_k_cache, host_v_cache, up(host_block_table), up(share.gpu_lens),
-                 softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
+        # rows by decreasing GPU work when the HBM lengths are known on the host
+            order = None
+        if not hbm_lens.is_cuda:
+            work = hbm_lens.numpy().astype(np.int64) + share.gpu_lens.numpy()
+            order = up("order", torch.from_numpy(
+                np.argsort(-work, kind="stable").astype(np.int32)))
+        o_gpu = torch.empty(n, H, D, dtype=torch.float32, device=dev)
+        l_gpu = torch.empty(H, n, dtype=torch.float32, device=dev)
+        split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table),
+                     up("hbm_lens", hbm_lens), host_k_cache, host_v_cache,
+                     up("host_bt", host_block_table), up("gpu_lens", share.gpu_lens),
+                     softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
+    except BaseException:
+        HYBRID_STAGING.release(idx, stream)
+        raise
     gpu_done = torch.cuda.Event()
-    gpu_done.record(torch.cuda.current_stream(dev))
+    gpu_done.record(stream)
     return HybridSplit(out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
-                       host_v_cache, share, softmax_scale, num_threads)
+                       host_v_cache, share, softmax_scale, num_threads, staging_idx=idx)
 
 
 def hybrid_split_decode(
