@@ -145,7 +145,8 @@ def test_forward_split_matches_unified_attention(gpu, prefill_ops, case, H, KVH,
     dp = plan.to_device(hp, sc.bt.to(gpu), gpu)
     state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k}, v={"l0": sc.host_v})
     impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, fused_split=mode != "two_partials",
-                                   cpu_fraction=0.6 if mode == "hybrid" else 0.0)
+                                   cpu_fraction=0.6 if mode == "hybrid" else 0.0,
+                                   hybrid_min_host_bytes=0)
     layer = SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None)
     output = torch.full_like(sc.query, float("nan"))
     impl._forward_split(layer, sc.query, sc.key, sc.value, sc.kv_cache, dp, output)

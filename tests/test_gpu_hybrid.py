@@ -111,3 +111,42 @@ def test_hybrid_sees_kv_written_by_the_gpu(gpu):
             assert torch.equal(c["hk"][b, :, t], k_new[i]) and torch.equal(c["hv"][b, :, t], v_new[i])
     ref_o, ref_l = oracle_merged(c)
     check(out, lse, ref_o, ref_l, c["lens"])
+
+
+def test_backend_uses_the_hybrid_only_above_its_host_bytes_threshold(gpu, monkeypatch):
+    """SplitDecodeImpl's default ("auto" share) sends a layer's host tier to
+    the host cores only when it holds at least hybrid_min_host_bytes of KV;
+    below that the fused GPU launch reads it. Both give the reference output."""
+    from types import SimpleNamespace
+
+    from tests.test_gpu_forward import REQS16, TOL, _PrefillOps, build_tiers
+    from vllm_fastdecoder_amd import backend, plan, state
+
+    monkeypatch.setattr(backend, "OPS", _PrefillOps)
+    calls = []
+    real_begin = ops.hybrid_split_begin
+
+    def spy(*a, **k):
+        calls.append(a[10])  # the share
+        return real_begin(*a, **k)
+
+    monkeypatch.setattr(ops, "hybrid_split_begin", spy)
+    G, C, H, KVH, D, BS, dtype = 24, 40, 8, 2, 128, 16, torch.float16
+    for threshold, expect_hybrid in ((1 << 40, False), (0, True)):
+        sc = build_tiers(REQS16, G, C, H, KVH, D, BS, dtype, 1, gpu)
+        hp = plan.build_host_plan(sc.qsl, sc.seq, sc.bt, sc.slots, G, C, BS)
+        dp = plan.to_device(hp, sc.bt.to(gpu), gpu)
+        state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k},
+                                        v={"l0": sc.host_v})
+        impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, hybrid_min_host_bytes=threshold)
+        assert impl.cpu_fraction == "auto"
+        calls.clear()
+        out = torch.full_like(sc.query, float("nan"))
+        impl._forward_split(SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None),
+                            sc.query, sc.key, sc.value, sc.kv_cache, dp, out)
+        torch.cuda.synchronize()
+        assert (len(calls) == 1) == expect_hybrid
+        if expect_hybrid:
+            assert calls[0] == 0.75  # the tuner's starting share
+        assert float((out.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
+    state.STORE = None

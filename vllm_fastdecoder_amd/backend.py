@@ -14,10 +14,13 @@ vLLM's base classes:
     one device-to-host copy of the step's block table and slots, the host
     planner, then the device plan.
   * `SplitDecodeImpl._forward_split` -- FastDecodeImpl._forward_split
-    (backend.py:257-357). The structure is the reference's; the host tier is
-    no longer computed on the host: its KV rows are written into the pinned
-    tier by the GPU and its partial is read zero-copy by the GPU, so there is
-    no staging copy and no host wait.
+    (backend.py:257-357). The structure is the reference's. The host tier's
+    KV rows are written into the pinned tier by the GPU (no staging copy);
+    its partial is shared between the host cores (each row's trailing host
+    blocks, as in the reference) and the GPU reading the rest zero-copy, the
+    share balanced online (`cpu_fraction="auto"`, the default); a layer with
+    little host-tier KV, or `cpu_fraction=0`, leaves the whole host tier to
+    the GPU with no host wait.
   * `build_device_step` / `SplitDecodeImpl._forward_device` -- this build's
     addition: the same step planned on the GPU (fd_plan_tiers), with no
     device-to-host copy, for steps whose prefill rows (if any) are fresh.
@@ -190,7 +193,11 @@ class SplitDecodeImpl:
     # only). 0 = the GPU reads the whole host tier; 1 = the reference's
     # division (the host cores compute the whole host-tier partial); "auto" =
     # balanced online from each step's finishing order (plan.ShareTuner).
-    cpu_fraction: float | str = 0.0
+    cpu_fraction: float | str = "auto"
+    # below this many bytes of host-tier KV in a layer the GPU alone reads the
+    # host tier: the host share's fixed cost (q to the host, one wait, the
+    # merge) outweighs what it saves
+    hybrid_min_host_bytes: int = 32 << 20
 
     def __post_init__(self) -> None:
         self._tuner = None
@@ -235,6 +242,11 @@ class SplitDecodeImpl:
         fused = self.fused_split and getattr(OPS, "split_decode", None) is not None
         hybrid = None
         share = self._host_share()
+        if share > 0 and ns:
+            host_bytes = (int(hp.s_cpu_lens.sum()) * 2 * self.num_kv_heads * self.head_size *
+                          query.element_size())
+            if host_bytes < self.hybrid_min_host_bytes:
+                share = 0.0
         if ns and fused and share > 0:
             # the GPU's share is enqueued now; the host cores run after the P
             # and F launches below, so those queue behind it on the GPU
