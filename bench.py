@@ -52,6 +52,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split-run", action="store_true")
     ap.add_argument("--cpu-iters", type=int, default=20)
+    ap.add_argument("--hybrid-profile", type=float, default=None, metavar="SHARE",
+                    help="only run hybrid split steps of the workload's split layout at this "
+                         "host-core share (for a kernel trace of their GPU side)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the 16-byte stream-copy kernel over MIB MiB (counter calibration)")
     return ap.parse_args()
@@ -220,21 +223,18 @@ def threads_used():
     return int(_lib.load_lib().fd_host_decode_threads())
 
 
-def split_run(w, lens, bt, q, steps, warmup, stream):
-    """60% of each row's blocks (the last ones) in pinned host memory, the rest
-    in HBM: HBM partial + host partial (zero-copy) + LSE merge, and the same
-    step as one fused launch (ops.split_decode)."""
+def split_tiers(w, lens, bt, dev):
+    """The split-run layout: 60% of each row's blocks (the last ones) in
+    pinned host memory [C, KVH, BS, D], the rest in the HBM tier's vLLM
+    layout, each tier's tables compacted (seeded N(0,1) data)."""
     import torch
 
     from tests import cases
-    from vllm_fastdecoder_amd import ops
     from vllm_fastdecoder_amd.pinned import pinned_empty
 
-    dev = q.device
     nb = (lens + w.BS - 1) // w.BS
     n_host = torch.ceil(nb.double() * 0.6).to(torch.int32)
     n_hbm = nb - n_host
-    last = lens - (nb - 1) * w.BS
     W = bt.shape[1]
     bt_g = torch.zeros(w.n, W, dtype=torch.int32)
     bt_c = torch.zeros(w.n, W, dtype=torch.int32)
@@ -249,7 +249,6 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         bt_c[i, :b] = torch.arange(pc, pc + b, dtype=torch.int32)
         pg += a
         pc += b
-    del last
     kc_g, vc_g, kv = cases.kv_pool(w, max(G, 1), "vllm", dev)
     hk = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
     hv = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
@@ -260,6 +259,48 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         for s in range(0, C, slab):
             e = min(C, s + slab)
             t[s:e].copy_(torch.randn(e - s, w.KVH, w.BS, w.D, generator=gen, device=dev).to(w.dtype).cpu())
+    return dict(bt_g=bt_g, bt_c=bt_c, len_g=len_g, len_c=len_c, G=G, C=C, kc_g=kc_g, vc_g=vc_g,
+                kv=kv, hk=hk, hv=hv)
+
+
+def hybrid_profile(w, lens, bt, q, frac, steps, warmup, stream):
+    """Only hybrid split steps at a fixed host-core share (for a kernel trace
+    of the GPU side): per-step time and the host cores' time."""
+    import torch
+
+    from vllm_fastdecoder_amd import ops
+
+    t = split_tiers(w, lens, bt, q.device)
+    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=q.device)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=q.device)
+    bt_g_d = t["bt_g"].to(q.device)
+    cpu_s = []
+
+    def step():
+        h = ops.hybrid_split_begin(q, t["kc_g"], t["vc_g"], bt_g_d, t["len_g"], t["hk"], t["hv"],
+                                   t["bt_c"], t["len_c"], w.scale, frac, out=out, lse=lse)
+        h.finish()
+        cpu_s.append(h.cpu_seconds)
+
+    ms = time_gpu(step, steps, warmup, stream)
+    cpu_ms = sum(cpu_s[warmup:]) / max(1, len(cpu_s) - warmup) * 1e3
+    return {"workload": w.name, "cpu_fraction": frac, "steps": steps, "step_ms": round(ms, 3),
+            "host_cores_ms": round(cpu_ms, 3), "host_cores": threads_used()}
+
+
+def split_run(w, lens, bt, q, steps, warmup, stream):
+    """The split-run layout (split_tiers): HBM partial + host partial
+    (zero-copy) + LSE merge, the same step as one fused launch
+    (ops.split_decode), the host cores alone, and the hybrid split."""
+    import torch
+
+    from vllm_fastdecoder_amd import ops
+
+    dev = q.device
+    t = split_tiers(w, lens, bt, dev)
+    bt_g, bt_c, len_g, len_c = t["bt_g"], t["bt_c"], t["len_g"], t["len_c"]
+    G, C, kc_g, vc_g, kv, hk, hv = (t[k] for k in ("G", "C", "kc_g", "vc_g", "kv", "hk", "hv"))
+    del t
     bt_g_d, bt_c_d = bt_g.to(dev), bt_c.to(dev)
     len_g_d, len_c_d = len_g.to(dev), len_c.to(dev)
     ord_g, ord_c = ops.longest_first(len_g).to(dev), ops.longest_first(len_c).to(dev)
@@ -389,6 +430,10 @@ def main() -> int:
         return copy_calibration(args.copy_calibration, args.steps, args.warmup)
     w = cases.WORKLOADS[args.workload]
     lens, bt, pool = cases.draw_lens_and_tables(w)
+    if args.hybrid_profile is not None:
+        print(json.dumps(hybrid_profile(w, lens, bt, cases.queries(w, dev), args.hybrid_profile,
+                                        args.steps, args.warmup, torch.cuda.current_stream(dev))))
+        return 0
     if args.layout == "vllm":
         kc, vc, _keep = cases.kv_pool(w, pool, "vllm", dev)
     else:
