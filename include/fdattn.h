@@ -334,6 +334,21 @@ int fd_host_decode_threads(void);
  * the extension's set_num_threads (cpu_attn.cpp:521). */
 int fd_host_set_threads(int32_t n);
 
+/* Division of each row's host-tier blocks between the GPU and the host cores
+ * for the hybrid split (host code; no counterpart in the reference, whose
+ * host cores take every host block, i.e. cpu_fraction = 1). For row r with
+ * nb = ceil(host_lens[r] / block_size) blocks, the host cores get its last
+ * k = min(floor(nb * cpu_fraction + 1/2), nb) blocks and the GPU the rest:
+ *   gpu_lens[r] = k ? (nb - k) * block_size : host_lens[r]  (whole blocks),
+ *   cpu_lens[r] = host_lens[r] - gpu_lens[r],
+ *   cpu_bt[r, 0 .. k) = host_bt[r, nb - k .. nb), then zeros up to bt_width.
+ * The GPU keeps host_bt itself. *cpu_width (may be NULL) = the largest k.
+ * A row needing more than bt_width blocks is FD_ERR_INVALID. */
+int fd_share_host_blocks(const int32_t* host_bt, int64_t bt_stride, int32_t bt_width,
+                         const int32_t* host_lens, int32_t n, int32_t block_size,
+                         double cpu_fraction, int32_t* gpu_lens, int32_t* cpu_bt,
+                         int64_t cpu_bt_stride, int32_t* cpu_lens, int32_t* cpu_width);
+
 /* Host-tier slot write on the host cores: the reference's store_kv
  * (cpu_attn.cpp:491-517, body :413-431) with host pointers.
  *   cache[slot / BS][kv head][slot % BS][:] = k[j][kv head][:]  (and V)

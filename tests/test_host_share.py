@@ -105,3 +105,16 @@ def test_share_tuner_bounds_and_backend_validation():
     for bad in (1.5, -0.1, "fast"):
         with pytest.raises(ValueError):
             backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction=bad)
+
+
+def test_share_rejects_rows_past_their_table_and_handles_empty_tables():
+    bt = torch.tensor([[1, 2], [3, 4]], dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="needs 3 blocks"):
+        share_host_blocks(bt, torch.tensor([16, 33], dtype=torch.int32), 16, 0.5)
+    s = share_host_blocks(torch.zeros(3, 0, dtype=torch.int32), torch.zeros(3, dtype=torch.int32),
+                          16, 0.7)
+    assert s.gpu_lens.tolist() == [0, 0, 0] and s.cpu_lens.tolist() == [0, 0, 0]
+    # negative lengths count as empty rows
+    s = share_host_blocks(bt, torch.tensor([-5, 20], dtype=torch.int32), 16, 1.0)
+    assert s.gpu_lens.tolist() == [0, 0] and s.cpu_lens.tolist() == [0, 20]
+    assert s.cpu_bt[1].tolist() == [3, 4]

@@ -11,7 +11,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
-from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 
 from .build import LIB_PATH
 
@@ -141,6 +141,15 @@ SIGNATURES: dict[str, tuple] = {
     "fd_host_decode_threads": (c_int, []),
     "fd_host_decode_isa": (c_int, []),
     "fd_host_set_threads": (c_int, [c_int32]),
+    "fd_share_host_blocks": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int32,            # host_bt, bt_stride, bt_width
+            c_void_p, c_int32, c_int32, c_double,  # host_lens, n, block_size, cpu_fraction
+            c_void_p, c_void_p, c_int64, c_void_p,  # gpu_lens, cpu_bt, cpu_bt_stride, cpu_lens
+            POINTER(c_int32),                      # cpu_width
+        ],
+    ),
     "fd_host_store_kv": (
         c_int,
         [

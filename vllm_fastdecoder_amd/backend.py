@@ -253,7 +253,9 @@ class SplitDecodeImpl:
             qs = query.index_select(0, dp.s_tok)
             hybrid = ops.hybrid_split_begin(qs, key_cache, value_cache, dp.s_gpu_bt_all,
                                             hp.s_gpu_lens, k_host, v_host, hp.s_cpu_bt,
-                                            hp.s_cpu_lens, float(self.scale), share)
+                                            hp.s_cpu_lens, float(self.scale), share,
+                                            hbm_lens_dev=dp.s_gpu_lens_all,
+                                            host_block_table_dev=dp.s_cpu_bt)
         elif ns and fused:
             qs = query.index_select(0, dp.s_tok)
             merged, _ = OPS.split_decode(qs, key_cache, value_cache, dp.s_gpu_bt_all,

@@ -422,6 +422,39 @@ using namespace fd;
 
 extern "C" int fd_host_decode_threads(void) { return default_threads(); }
 
+extern "C" int fd_share_host_blocks(const int32_t* host_bt, int64_t bt_stride, int32_t bt_width,
+                                    const int32_t* host_lens, int32_t n, int32_t block_size,
+                                    double cpu_fraction, int32_t* gpu_lens, int32_t* cpu_bt,
+                                    int64_t cpu_bt_stride, int32_t* cpu_lens,
+                                    int32_t* cpu_width) {
+  if (n < 0 || bt_width < 0 || block_size <= 0 || !(cpu_fraction >= 0.0 && cpu_fraction <= 1.0))
+    return set_error(FD_ERR_INVALID, "fd_share_host_blocks: bad sizes or fraction");
+  if (n > 0 && (!host_lens || !gpu_lens || !cpu_lens || (bt_width > 0 && (!host_bt || !cpu_bt))))
+    return set_error(FD_ERR_INVALID, "fd_share_host_blocks: NULL pointer");
+  if (n > 0 && (bt_stride < bt_width || cpu_bt_stride < bt_width))
+    return set_error(FD_ERR_INVALID, "fd_share_host_blocks: row stride below the table width");
+  int32_t wc = 0;
+  for (int32_t r = 0; r < n; ++r) {
+    const int64_t len = std::max<int32_t>(host_lens[r], 0);
+    const int64_t nb = (len + block_size - 1) / block_size;
+    if (nb > bt_width)
+      return set_error(FD_ERR_INVALID, "fd_share_host_blocks: row %d needs %lld blocks > width %d",
+                       r, (long long)nb, bt_width);
+    const int64_t k = std::min<int64_t>((int64_t)std::floor((double)nb * cpu_fraction + 0.5), nb);
+    const int64_t j0 = nb - k;
+    gpu_lens[r] = (int32_t)(k > 0 ? j0 * block_size : len);
+    cpu_lens[r] = (int32_t)(len - gpu_lens[r]);
+    if (bt_width > 0) {
+      int32_t* dst = cpu_bt + (int64_t)r * cpu_bt_stride;
+      if (k > 0) memcpy(dst, host_bt + (int64_t)r * bt_stride + j0, (size_t)k * 4);
+      if (bt_width > k) memset(dst + k, 0, (size_t)(bt_width - k) * 4);
+    }
+    wc = std::max<int32_t>(wc, (int32_t)k);
+  }
+  if (cpu_width) *cpu_width = wc;
+  return FD_OK;
+}
+
 extern "C" int fd_host_set_threads(int32_t n) {
   g_threads.store(n > 0 ? n : 0, std::memory_order_relaxed);
   return FD_OK;

@@ -381,10 +381,15 @@ def hybrid_split_begin(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     num_threads: int = 0,
+    hbm_lens_dev: torch.Tensor | None = None,
+    host_block_table_dev: torch.Tensor | None = None,
 ) -> HybridSplit:
     """First half of hybrid_split_decode: divides the host tier, starts the
     copy of q to the host and enqueues the GPU's fused launch. Other GPU work
-    can be enqueued before HybridSplit.finish()."""
+    can be enqueued before HybridSplit.finish(). hbm_lens_dev /
+    host_block_table_dev: device copies of hbm_lens / host_block_table the
+    caller already holds (the GPU's share reads the host table unchanged,
+    only with shorter lengths), saving their uploads."""
     _require(q.is_cuda and q.dim() == 3, "q must be [n, H, D] on the GPU")
     _require(host_block_table.device.type == "cpu" and host_lens.device.type == "cpu",
              "host_block_table and host_lens must be CPU tensors")
@@ -419,9 +424,11 @@ def hybrid_split_begin(
                 np.argsort(-work, kind="stable").astype(np.int32)))
         o_gpu = torch.empty(n, H, D, dtype=torch.float32, device=dev)
         l_gpu = torch.empty(H, n, dtype=torch.float32, device=dev)
-        split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table),
-                     up("hbm_lens", hbm_lens), host_k_cache, host_v_cache,
-                     up("host_bt", host_block_table), up("gpu_lens", share.gpu_lens),
+        hl = hbm_lens_dev if hbm_lens_dev is not None else up("hbm_lens", hbm_lens)
+        hbt = (host_block_table_dev if host_block_table_dev is not None
+               else up("host_bt", host_block_table))
+        split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table), hl,
+                     host_k_cache, host_v_cache, hbt, up("gpu_lens", share.gpu_lens),
                      softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
     except BaseException:
         HYBRID_STAGING.release(idx, stream)

@@ -29,8 +29,6 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-import numpy as np
-
 import torch
 
 GPU_TABLE_PAD = 16  # HBM-tier tables are padded to a multiple of 16 columns (plan.py:171,195-201)
@@ -297,28 +295,26 @@ def share_host_blocks(host_bt: torch.Tensor, host_lens: torch.Tensor, block_size
     out."""
     if not 0.0 <= cpu_fraction <= 1.0:
         raise ValueError(f"cpu_fraction must be in [0, 1], got {cpu_fraction}")
-    # numpy, single-threaded on purpose: this runs once per layer right before
-    # the host cores' share, and torch's parallel CPU ops leave their OpenMP
-    # team spinning on the very cores that share needs
-    bt = host_bt.numpy()
-    lens = np.maximum(host_lens.numpy().astype(np.int64), 0)
+    # one pass of host code in the library (fd_share_host_blocks): this runs
+    # once per layer right before the host cores' share, so it stays cheap and
+    # single-threaded (torch's parallel CPU operators leave their OpenMP team
+    # spinning on the very cores that share needs)
+    import ctypes
+
+    from . import _lib
+
+    bt = host_bt.contiguous() if host_bt.stride(-1) != 1 else host_bt
+    lens = host_lens.to(torch.int32).contiguous()
     n, W = bt.shape
-    nb = (lens + block_size - 1) // block_size
-    k_cpu = np.minimum(np.floor(nb * float(cpu_fraction) + 0.5).astype(np.int64), nb)
-    j0 = nb - k_cpu
-    gpu_lens = np.where(k_cpu > 0, j0 * block_size, lens)
-    cpu_lens = lens - gpu_lens
-    wc = int(k_cpu.max()) if n else 0
-    cols = np.arange(max(wc, 1), dtype=np.int64)
-    if W:
-        src = np.minimum(j0[:, None] + cols[None, :], W - 1)
-        cpu_bt = np.take_along_axis(bt, src, axis=1)
-    else:
-        cpu_bt = np.zeros((n, cols.size), dtype=np.int32)
-    cpu_bt = np.where(cols[None, :] < k_cpu[:, None], cpu_bt, 0).astype(np.int32)
-    return HostShare(torch.from_numpy(gpu_lens.astype(np.int32)),
-                     torch.from_numpy(np.ascontiguousarray(cpu_bt)),
-                     torch.from_numpy(cpu_lens.astype(np.int32)))
+    gpu_lens = torch.empty(n, dtype=torch.int32)
+    cpu_lens = torch.empty(n, dtype=torch.int32)
+    cpu_bt = (torch.empty if W else torch.zeros)(n, max(W, 1), dtype=torch.int32)
+    wc = ctypes.c_int32(0)
+    _lib.check(_lib.load_lib().fd_share_host_blocks(
+        bt.data_ptr(), bt.stride(0) if n else W, W, lens.data_ptr(), n, block_size,
+        float(cpu_fraction), gpu_lens.data_ptr(), cpu_bt.data_ptr(), cpu_bt.stride(0),
+        cpu_lens.data_ptr(), ctypes.byref(wc)))
+    return HostShare(gpu_lens, cpu_bt[:, :max(wc.value, 1)], cpu_lens)
 
 
 class ShareTuner:
