@@ -150,3 +150,34 @@ def test_backend_uses_the_hybrid_only_above_its_host_bytes_threshold(gpu, monkey
             assert calls[0] == 0.75  # the tuner's starting share
         assert float((out.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
     state.STORE = None
+
+
+def test_two_micro_batches_interleaved_with_other_gpu_work(gpu):
+    """Micro-batch overlap with the begin / finish halves: begin(A), enqueue
+    other GPU work, finish(A), begin(B), other work, finish(B). One hybrid
+    split in flight per device; a second begin before finish is refused.
+    Both micro-batches give the oracle's result."""
+    ca = two_tier_case(10, 16, 4, 128, torch.float16, seed=21, dev=gpu)
+    cb = two_tier_case(7, 16, 4, 128, torch.float16, seed=22, dev=gpu)
+    x = torch.randn(2048, 2048, device=gpu)
+    outs = []
+    for c in (ca, cb):
+        q = c["q"].to(gpu)
+        n, H, D = q.shape
+        out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+        h = ops.hybrid_split_begin(q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"],
+                                   c["hk"], c["hv"], c["bt_c"], c["len_c"], c["scale"], 0.6,
+                                   out=out, lse=lse)
+        with pytest.raises(RuntimeError, match="in flight"):
+            ops.hybrid_split_begin(q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"],
+                                   c["hk"], c["hv"], c["bt_c"], c["len_c"], c["scale"], 0.6)
+        for _ in range(4):  # the other micro-batch's GPU work
+            x = torch.tanh(x @ x) * 0.01
+        h.finish()
+        outs.append((out, lse))
+    torch.cuda.synchronize()
+    assert torch.isfinite(x).all()
+    for c, (out, lse) in zip((ca, cb), outs):
+        ref_o, ref_l = oracle_merged(c)
+        check(out, lse, ref_o, ref_l, c["lens"])
