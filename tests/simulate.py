@@ -95,7 +95,8 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
     uphys = (torch.randn(G + C, BS, KVH, 2 * D, device=dev) * 10).to(dtype)
     ukc, uvc = uphys[..., :D], uphys[..., D:]
     impl = backend.SplitDecodeImpl(H, KVH, D, scale, fused_split=fused, cpu_fraction=cpu_fraction,
-                                   hybrid_min_host_bytes=0)
+                                   hybrid_min_host_bytes=0,
+                                   device_step_hybrid=planner == "device" and cpu_fraction != 0.0)
 
     free_gpu = list(range(1, G))
     free_host = list(range(G, G + C))

@@ -202,7 +202,8 @@ def test_hipops_fa_rejects_prefill_forms(gpu):
 
 @pytest.mark.parametrize("fused,planner,cpu_fraction",
                          [(True, "host", 0.0), (False, "host", 0.0), (True, "device", 0.0),
-                          (True, "host", 0.6), (True, "host", "auto")])
+                          (True, "host", 0.6), (True, "host", "auto"),
+                          (True, "device", "auto")])
 def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
     """The config of the reference's GPU self-test at vicuna-7b head shapes:
     300 decode steps, G=256 HBM blocks, C=2048 host blocks, Poisson(4)
@@ -212,7 +213,8 @@ def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
     rows through the fused launch and through two partials + merge, with the
     step planned on the host (one device-to-host copy per step, as in the
     reference) or on the GPU (none); and the fused launch with 60% of each
-    row's host blocks reduced by the host cores (hybrid split)."""
+    row's host blocks reduced by the host cores (hybrid split), or the share
+    balanced online, with either planner."""
     from tests.simulate import run_simulation
 
     stats = run_simulation(steps=300, seed=4, device=gpu, fused=fused, planner=planner,

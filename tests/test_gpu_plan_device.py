@@ -181,3 +181,41 @@ def test_device_planned_decode_step_never_waits_for_the_gpu(gpu, monkeypatch):
     torch.cuda.synchronize()
     state.STORE = None
     assert float((out.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_forward_device_hybrid(gpu, dtype, monkeypatch):
+    """device_step_hybrid: the decode rows' host tier shared with the host
+    cores in a GPU-planned step (one copy of their tables per step, reused by
+    every layer); the reference output, and the tables fetched once across
+    two layers."""
+    monkeypatch.setattr(backend, "OPS", _PrefillOps)
+    G, C, BS, H, KVH, D = 24, 40, 16, 8, 2, 128
+    sc = build_tiers(REQS16, G, C, H, KVH, D, BS, dtype, 1, gpu)
+    state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k, "l1": sc.host_k},
+                                    v={"l0": sc.host_v, "l1": sc.host_v})
+    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale, device_step_hybrid=True,
+                                   hybrid_min_host_bytes=0)
+    calls = []
+    real_begin = ops.hybrid_split_begin
+    monkeypatch.setattr(ops, "hybrid_split_begin",
+                        lambda *a, **k: calls.append(1) or real_begin(*a, **k))
+    R = sc.bt.shape[0]
+    ds = backend.build_device_step(sc.qsl, sc.seq, sc.bt.to(gpu), sc.slots.to(gpu), R,
+                                   state.STORE, gpu)
+    assert ds is not None and ds.n_dec > 0
+    out = torch.full_like(sc.query, float("nan"))
+    impl._forward_device(SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None),
+                         sc.query, sc.key, sc.value, sc.kv_cache, ds, out)
+    fetched = ds._host
+    assert fetched is not None and len(calls) == 1
+    # a second layer of the same step reuses the fetched tables (its KV
+    # writes land on the same slots with the same values)
+    out2 = torch.full_like(sc.query, float("nan"))
+    impl._forward_device(SimpleNamespace(layer_name="l1", _k_scale=None, _v_scale=None),
+                         sc.query, sc.key, sc.value, sc.kv_cache, ds, out2)
+    assert ds._host is fetched and len(calls) == 2
+    torch.cuda.synchronize()
+    state.STORE = None
+    for o in (out, out2):
+        assert float((o.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]

@@ -28,7 +28,7 @@ vLLM's base classes:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -128,6 +128,22 @@ class DeviceStep:
     f_max: int
     n_f_tok: int
     errors: torch.Tensor  # [1] int32: host ids past the tier, lengths past the table
+    # the decode rows' host-tier view, fetched once per step for the hybrid
+    # split (host_tables)
+    _host: tuple | None = field(default=None, repr=False)
+
+    def host_tables(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(hbm_lens, host_bt, host_lens) of the decode rows on the host: one
+        device-to-host copy per step (waits for the planning kernels), reused
+        by every layer."""
+        if self._host is None:
+            rows = self.dec_rows
+            packed = torch.cat([self.gpu_lens.index_select(0, rows)[:, None],
+                                self.cpu_lens.index_select(0, rows)[:, None],
+                                self.cpu_bt.index_select(0, rows)], dim=1).cpu()
+            self._host = (packed[:, 0].contiguous(), packed[:, 2:].contiguous(),
+                          packed[:, 1].contiguous())
+        return self._host
 
 
 def build_device_step(query_start_loc_cpu: torch.Tensor, seq_lens_cpu: torch.Tensor,
@@ -198,6 +214,11 @@ class SplitDecodeImpl:
     # host tier: the host share's fixed cost (q to the host, one wait, the
     # merge) outweighs what it saves
     hybrid_min_host_bytes: int = 32 << 20
+    # the hybrid split in steps planned on the GPU (_forward_device) too: one
+    # device-to-host copy of the decode rows' tables per step, and the per-layer
+    # wait for q the host share needs; off by default, so that such steps keep
+    # the GPU planner's no-wait property
+    device_step_hybrid: bool = False
 
     def __post_init__(self) -> None:
         self._tuner = None
@@ -317,7 +338,9 @@ class SplitDecodeImpl:
         """The step of _forward_split planned on the GPU (build_device_step):
         KV writes into both tiers from the split slot mapping, every decode row
         (all-HBM and split alike) through one fused two-tier launch, fresh
-        prefills through the prefill form of OPS.fa. No device-to-host copy."""
+        prefills through the prefill form of OPS.fa. No device-to-host copy,
+        unless device_step_hybrid gives the decode rows' host tier to the
+        hybrid split (one copy of their tables per step)."""
         store = state.STORE
         assert store is not None, "no host KV tier (state.ensure_store)"
         k_host = store.k[layer.layer_name]
@@ -334,16 +357,28 @@ class SplitDecodeImpl:
                                   ds.host_slots)
 
         # 2) decode rows: both tiers in one launch (a row without host tokens
-        #    is plain paged attention over its HBM blocks)
+        #    is plain paged attention over its HBM blocks), or, with
+        #    device_step_hybrid, the hybrid split of that launch
+        hybrid = None
         if ds.n_dec:
             q = query.index_select(0, ds.dec_tok)
-            out, _ = OPS.split_decode(q, key_cache, value_cache,
-                                      ds.gpu_bt.index_select(0, ds.dec_rows),
-                                      ds.gpu_lens.index_select(0, ds.dec_rows), k_host, v_host,
-                                      ds.cpu_bt.index_select(0, ds.dec_rows),
-                                      ds.cpu_lens.index_select(0, ds.dec_rows),
-                                      float(self.scale), row_order=ds.dec_order)
-            output.index_copy_(0, ds.dec_tok, out)
+            gbt = ds.gpu_bt.index_select(0, ds.dec_rows)
+            gl = ds.gpu_lens.index_select(0, ds.dec_rows)
+            cbt = ds.cpu_bt.index_select(0, ds.dec_rows)
+            share = self._host_share() if self.device_step_hybrid else 0.0
+            if share > 0:
+                hl_h, cbt_h, cl_h = ds.host_tables()
+                host_bytes = (int(cl_h.sum()) * 2 * self.num_kv_heads * self.head_size *
+                              query.element_size())
+                if host_bytes >= self.hybrid_min_host_bytes:
+                    hybrid = ops.hybrid_split_begin(q, key_cache, value_cache, gbt, hl_h, k_host,
+                                                    v_host, cbt_h, cl_h, float(self.scale), share,
+                                                    hbm_lens_dev=gl, host_block_table_dev=cbt)
+            if hybrid is None:
+                out, _ = OPS.split_decode(q, key_cache, value_cache, gbt, gl, k_host, v_host, cbt,
+                                          ds.cpu_lens.index_select(0, ds.dec_rows),
+                                          float(self.scale), row_order=ds.dec_order)
+                output.index_copy_(0, ds.dec_tok, out)
 
         # 3) fresh prefills attend only this step's q/k/v (backend.py:331-340)
         if ds.n_f_tok:
@@ -356,4 +391,9 @@ class SplitDecodeImpl:
                 causal=True, softcap=self.logits_soft_cap,
             )
             output.index_copy_(0, ds.f_tok, o_f)
+        if hybrid is not None:  # the host cores' share, while the GPU runs the above
+            out, _ = hybrid.finish()
+            if self._tuner is not None:
+                self._tuner.update(hybrid.gpu_finished_first)
+            output.index_copy_(0, ds.dec_tok, out)
         return output
