@@ -161,6 +161,19 @@ def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
     times.sort()
     t = times[len(times) // 2]
     _, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    # this library's host-core kernel (fd_host_decode_partial) on the same
+    # data and cores, for comparison with the reference's
+    from vllm_fastdecoder_amd import ops
+
+    ours = []
+    out_h = torch.empty(w.n, w.H, w.D, dtype=w.dtype)
+    for i in range(3 + min(iters, len(times))):
+        t0 = time.perf_counter()
+        ops.host_decode_attn(q_cpu, k, v, bt, lens, w.scale, out_h, lse, num_threads=cores)
+        if i >= 3:
+            ours.append(time.perf_counter() - t0)
+    ours.sort()
+    t_ours = ours[len(ours) // 2]
     del k, v
     return {
         "value": round(kvb / t / 1e9, 2),
@@ -174,6 +187,9 @@ def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
                       if kind == "reference" else "restated fp32 two-pass C kernel")),
         "ms_per_call": round(t * 1e3, 3),
         "tokens_per_s": round(w.n / (t * LAYERS), 1),
+        "host_kernel": {"value": round(kvb / t_ours / 1e9, 2), "unit": "GB/s",
+                        "ms_per_call": round(t_ours * 1e3, 3),
+                        "note": "this library's fd_host_decode_partial, same data and cores"},
     }
 
 
