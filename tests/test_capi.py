@@ -169,3 +169,50 @@ def test_split_decode_null_descriptor_and_n_zero():
                                0, 96, 512, 64, 0, 112, 2, None, 0, None) == _lib.FD_ERR_INVALID
     # n == 0: nothing to do, even with NULL tier pointers
     assert _split(lib, hbm=_tier(k=None, lens=None), host=_tier(bt=None), n=0) == _lib.FD_OK
+
+
+def test_host_entry_points_reject_bad_arguments():
+    """fd_share_host_blocks / fd_host_store_kv / fd_host_set_threads through the
+    C ABI: every invalid call returns a status and writes nothing."""
+    import ctypes
+
+    import torch
+
+    lib = _lib.load_lib()
+    bt = torch.tensor([[1, 2], [3, 4]], dtype=torch.int32)
+    lens = torch.tensor([20, 5], dtype=torch.int32)
+    gl = torch.full((2,), -7, dtype=torch.int32)
+    cl = torch.full((2,), -7, dtype=torch.int32)
+    cbt = torch.full((2, 2), -7, dtype=torch.int32)
+    wc = ctypes.c_int32(-1)
+
+    def share(frac, stride=2, cstride=2, n=2, bs=16, bt_ptr=bt.data_ptr()):
+        return lib.fd_share_host_blocks(bt_ptr, stride, 2, lens.data_ptr(), n, bs, frac,
+                                        gl.data_ptr(), cbt.data_ptr(), cstride, cl.data_ptr(),
+                                        ctypes.byref(wc))
+
+    for bad in (share(1.5), share(-0.1), share(float("nan")), share(0.5, stride=1),
+                share(0.5, cstride=1), share(0.5, bs=0), share(0.5, n=-1), share(0.5, bt_ptr=None)):
+        assert bad == _lib.FD_ERR_INVALID
+    assert torch.all(gl == -7) and torch.all(cbt == -7) and wc.value == -1
+    assert share(0.5) == _lib.FD_OK
+    assert gl.tolist() == [16, 0] and cl.tolist() == [4, 5] and wc.value == 1
+    assert cbt[:, :1].tolist() == [[2], [3]] and int(cbt[0, 1]) == 0
+
+    kc = torch.zeros(2, 1, 16, 8, dtype=torch.float16)
+    k = torch.ones(1, 1, 8, dtype=torch.float16)
+    slots = torch.tensor([5], dtype=torch.int64)
+
+    def store(dtype=_lib.FD_F16, m=1, kvh=1, ptr=k.data_ptr()):
+        return lib.fd_host_store_kv(ptr, 8, 8, ptr, 8, 8, kc.data_ptr(), kc.data_ptr(),
+                                    kc.stride(0), kc.stride(1), kc.stride(2), 2,
+                                    slots.data_ptr(), m, kvh, 8, 16, dtype)
+
+    assert store(dtype=7) == _lib.FD_ERR_INVALID
+    assert store(m=-1) == _lib.FD_ERR_INVALID
+    assert store(kvh=0) == _lib.FD_ERR_INVALID
+    assert store(ptr=None) == _lib.FD_ERR_INVALID
+    assert store(m=0, ptr=None) == _lib.FD_OK  # nothing to write
+    assert not kc.any()
+    assert store() == _lib.FD_OK and kc[0, 0, 5].tolist() == [1.0] * 8
+    assert lib.fd_host_set_threads(0) == _lib.FD_OK
