@@ -29,6 +29,8 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
+
 import torch
 
 GPU_TABLE_PAD = 16  # HBM-tier tables are padded to a multiple of 16 columns (plan.py:171,195-201)
@@ -75,40 +77,50 @@ class HostPlan:
         return int(self.f_tok.numel())
 
 
-def _token_runs(starts: torch.Tensor, counts: torch.Tensor) -> torch.Tensor:
+# The planner's array work is numpy: single-threaded and cheap for a step's
+# few hundred rows. torch's parallel CPU operators would leave their OpenMP
+# team spinning on the host cores that the hybrid split's host share uses
+# next. Results are torch tensors, as in the reference.
+
+
+def _token_runs(starts: np.ndarray, counts: np.ndarray) -> np.ndarray:
     """The token indices start .. start + count - 1 of every run, in order."""
-    counts = counts.to(torch.int64)
-    total = int(counts.sum()) if counts.numel() else 0
+    counts = counts.astype(np.int64)
+    total = int(counts.sum()) if counts.size else 0
     if total == 0:
-        return torch.zeros(0, dtype=torch.int64)
-    run = torch.repeat_interleave(torch.arange(counts.numel()), counts)
-    first = torch.cumsum(counts, 0) - counts  # position of each run's first token
-    return starts.to(torch.int64)[run] + (torch.arange(total) - first[run])
+        return np.zeros(0, dtype=np.int64)
+    run = np.repeat(np.arange(counts.size), counts)
+    first = np.cumsum(counts) - counts  # position of each run's first token
+    return starts.astype(np.int64)[run] + (np.arange(total) - first[run])
 
 
-def _offsets(counts: torch.Tensor) -> torch.Tensor:
+def _offsets(counts: np.ndarray) -> np.ndarray:
     """[0, c0, c0 + c1, ...] as int32."""
-    out = torch.zeros(counts.numel() + 1, dtype=torch.int32)
-    if counts.numel():
-        out[1:] = torch.cumsum(counts.to(torch.int64), 0).to(torch.int32)
+    out = np.zeros(counts.size + 1, dtype=np.int32)
+    if counts.size:
+        out[1:] = np.cumsum(counts.astype(np.int64)).astype(np.int32)
     return out
 
 
-def compact_rows(table: torch.Tensor, keep: torch.Tensor, subtract: int, pad_to: int = 1) -> torch.Tensor:
+def compact_rows(table, keep, subtract: int, pad_to: int = 1) -> torch.Tensor:
     """Per row, the kept entries moved to the front in their original order,
     minus `subtract`; every other entry 0. Width: the largest kept count
-    (at least 1) rounded up to `pad_to` (fastdecode/plan.py:82-100)."""
+    (at least 1) rounded up to `pad_to` (fastdecode/plan.py:82-100). numpy
+    or torch CPU arrays in, an int32 torch tensor out."""
+    table = np.asarray(table)
+    keep = np.asarray(keep, dtype=bool)
     rows, width_in = table.shape
-    if table.numel() == 0:
+    if table.size == 0:
         return torch.zeros(rows, pad_to, dtype=torch.int32)
     per_row = keep.sum(1)
     width = max(1, int(per_row.max()))
     width = -(-width // pad_to) * pad_to
-    out = torch.zeros(rows, max(width, width_in), dtype=torch.int64)
-    r, c = keep.nonzero(as_tuple=True)  # row-major: stable inside each row
-    dest = (torch.cumsum(keep.to(torch.int64), 1) - 1)[r, c]
-    out[r, dest] = table[r, c].to(torch.int64) - subtract
-    return out[:, :width].to(torch.int32).contiguous()
+    vals = table[keep].astype(np.int64) - subtract  # row-major: stable inside each row
+    row = np.repeat(np.arange(rows, dtype=np.int64), per_row)
+    pos = np.arange(vals.size, dtype=np.int64) - np.repeat(np.cumsum(per_row) - per_row, per_row)
+    out = np.zeros(rows * width, dtype=np.int32)
+    out[row * width + pos] = vals
+    return torch.from_numpy(out.reshape(rows, width))
 
 
 def build_host_plan(
@@ -121,20 +133,20 @@ def build_host_plan(
     block_size: int,
 ) -> HostPlan | None:
     G, bs = int(num_gpu_blocks), int(block_size)
-    qsl = query_start_loc.to(torch.int64)
-    lens = seq_lens.to(torch.int64)
+    qsl = query_start_loc.numpy().astype(np.int64)
+    lens = seq_lens.numpy().astype(np.int64)
     qlen = qsl[1:] - qsl[:-1]
     prior = lens - qlen
-    n_tok = int(qsl[-1]) if qsl.numel() else 0
-    slots = slot_mapping[:n_tok].to(torch.int64)
+    n_tok = int(qsl[-1]) if qsl.size else 0
+    slots = slot_mapping.numpy()[:n_tok].astype(np.int64)
 
     R, W = block_table.shape
-    col = torch.arange(W, dtype=torch.int64)
+    col = np.arange(W, dtype=np.int64)
     # tokens held by column c of each row: bs for full blocks, the remainder
     # for the last one, 0 past the row's blocks
-    held = (lens[:, None] - col[None, :] * bs).clamp(min=0, max=bs)
+    held = np.clip(lens[:, None] - col[None, :] * bs, 0, bs)
     used = held > 0
-    ids = block_table.to(torch.int64)
+    ids = block_table.numpy().astype(np.int64)
     in_host = used & (ids >= G)
     in_hbm = used & (ids < G)
     touches_host = in_host.any(1)
@@ -143,7 +155,7 @@ def build_host_plan(
     if not bool(touches_host.any()) and not bool(host_slot.any()):
         return None  # everything in HBM this step: plain paged attention
 
-    if bool(in_host.any()) and int(ids[in_host].max()) >= G + int(num_cpu_blocks):
+    if int(np.max(ids, where=in_host, initial=-1)) >= G + int(num_cpu_blocks):
         raise RuntimeError(
             "FastDecode: block id beyond GPU+CPU capacity; engine and worker "
             "disagree on FASTDECODE_CPU_BLOCKS / FASTDECODE_CPU_KV_GB"
@@ -161,45 +173,47 @@ def build_host_plan(
         )
     is_p = active & ~touches_host
 
-    minus_one = torch.full_like(slots, -1)
-    gpu_slot_mapping = torch.where(host_slot, minus_one, slots)
-    host_slot_mapping = torch.where(host_slot, slots - G * bs, minus_one)
-    cpu_w_tok = host_slot.nonzero().flatten()
-    cpu_w_slot = (slots[cpu_w_tok] - G * bs).contiguous()
+    gpu_slot_mapping = np.where(host_slot, -1, slots)
+    host_slot_mapping = np.where(host_slot, slots - G * bs, -1)
+    cpu_w_tok = np.nonzero(host_slot)[0]
+    cpu_w_slot = slots[cpu_w_tok] - G * bs
 
-    p_req = is_p.nonzero().flatten()
+    p_req = np.nonzero(is_p)[0]
     p_q = qlen[p_req]
-    p_seqlens = lens[p_req].to(torch.int32)
+    p_seqlens = lens[p_req].astype(np.int32)
 
-    s_req = is_s.nonzero().flatten()
+    s_req = np.nonzero(is_s)[0]
     s_held = held[s_req]
-    s_gpu_lens = (s_held * in_hbm[s_req]).sum(1).to(torch.int32)
-    s_cpu_lens = (s_held * in_host[s_req]).sum(1).to(torch.int32).contiguous()
+    s_gpu_lens = (s_held * in_hbm[s_req]).sum(1).astype(np.int32)
+    s_cpu_lens = (s_held * in_host[s_req]).sum(1).astype(np.int32)
 
-    f_req = is_f.nonzero().flatten()
+    f_req = np.nonzero(is_f)[0]
     f_q = qlen[f_req]
+
+    def t(a: np.ndarray) -> torch.Tensor:
+        return torch.from_numpy(np.ascontiguousarray(a))
 
     return HostPlan(
         n_tok=n_tok,
-        gpu_slot_mapping=gpu_slot_mapping,
-        cpu_w_tok=cpu_w_tok,
-        cpu_w_slot=cpu_w_slot,
-        p_tok=_token_runs(qsl[p_req], p_q),
-        p_cu=_offsets(p_q),
-        p_seqlens=p_seqlens,
-        p_req=p_req,
-        p_max_q=int(p_q.max()) if p_q.numel() else 0,
-        p_max_k=int(p_seqlens.max()) if p_seqlens.numel() else 0,
-        s_tok=qsl[s_req],
+        gpu_slot_mapping=t(gpu_slot_mapping.astype(np.int64)),
+        cpu_w_tok=t(cpu_w_tok.astype(np.int64)),
+        cpu_w_slot=t(cpu_w_slot.astype(np.int64)),
+        p_tok=t(_token_runs(qsl[p_req], p_q)),
+        p_cu=t(_offsets(p_q)),
+        p_seqlens=t(p_seqlens),
+        p_req=t(p_req.astype(np.int64)),
+        p_max_q=int(p_q.max()) if p_q.size else 0,
+        p_max_k=int(p_seqlens.max()) if p_seqlens.size else 0,
+        s_tok=t(qsl[s_req]),
         s_gpu_bt=compact_rows(ids[s_req], in_hbm[s_req], 0, pad_to=GPU_TABLE_PAD),
-        s_gpu_lens=s_gpu_lens,
-        s_max_gpu_len=int(s_gpu_lens.max()) if s_gpu_lens.numel() else 0,
+        s_gpu_lens=t(s_gpu_lens),
+        s_max_gpu_len=int(s_gpu_lens.max()) if s_gpu_lens.size else 0,
         s_cpu_bt=compact_rows(ids[s_req], in_host[s_req], G),
-        s_cpu_lens=s_cpu_lens,
-        f_tok=_token_runs(qsl[f_req], f_q),
-        f_cu=_offsets(f_q),
-        f_max=int(f_q.max()) if f_q.numel() else 0,
-        host_slot_mapping=host_slot_mapping,
+        s_cpu_lens=t(s_cpu_lens),
+        f_tok=t(_token_runs(qsl[f_req], f_q)),
+        f_cu=t(_offsets(f_q)),
+        f_max=int(f_q.max()) if f_q.size else 0,
+        host_slot_mapping=t(host_slot_mapping.astype(np.int64)),
     )
 
 
