@@ -246,3 +246,19 @@ def test_fused_rejects_mismatched_tiers(gpu):
         ops.split_decode(q, c["kv"][..., :64], c["kv"][..., 64:], c["bt_g"].to(gpu),
                          c["len_g"].to(gpu), c["hk"][:, :4], c["hv"][:, :4], c["bt_c"].to(gpu),
                          c["len_c"].to(gpu), 0.1)  # host tier with 4 kv heads, HBM with 8
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_second_tier_in_hbm(gpu, dtype):
+    """Both tiers in device memory: the grouped-query launch stays on the
+    matrix-core kernel (a launch that reads pinned host memory takes the VALU
+    kernel instead); same oracle bars."""
+    c = two_tier_case(8, 32, 8, 128, dtype, seed=31, dev=gpu)
+    dev_tiers = dict(c, hk=c["hk"].to(gpu), hv=c["hv"].to(gpu))
+    out, lse = run_fused(dev_tiers, gpu)
+    ref, ref_lse = oracle.decode_attn_host_layout_f64(c["q"], c["pool_k"], c["pool_v"],
+                                                      c["full_bt"], c["lens"], c["scale"])
+    nz = c["lens"] > 0
+    check_vs_oracle(out, lse, ref, ref_lse, nz)
+    out_h, lse_h = run_fused(c, gpu)  # the same step reading the pinned host tier
+    assert float((out - out_h)[nz.to(gpu)].abs().max()) <= 2e-5

@@ -34,6 +34,28 @@ bool valid_dtype(int dt) { return dt == FD_F16 || dt == FD_BF16 || dt == FD_F32;
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
+// Whether p points into pinned host memory, which the GPU reads over the link.
+// The answer for each recently seen pointer is kept per thread (a lookup
+// costs ~1 us; a layer's caches keep their addresses), and a stale entry
+// after a free can only change which of two correct kernels runs.
+bool in_host_memory(const void* p) {
+  struct Entry {
+    const void* p;
+    bool host;
+  };
+  constexpr int kEntries = 128;
+  static thread_local Entry cache[kEntries] = {};
+  static thread_local int next = 0;
+  for (const Entry& e : cache)
+    if (e.p == p) return e.host;
+  hipPointerAttribute_t attr{};
+  const bool host = hipPointerGetAttributes(&attr, p) == hipSuccess && attr.type == hipMemoryTypeHost;
+  (void)hipGetLastError();  // a pointer the runtime does not know leaves no error behind
+  cache[next] = {p, host};
+  next = (next + 1) % kEntries;
+  return host;
+}
+
 // Validates a decode call over a.ntiers tiers (tiers already filled in),
 // completes `a` and launches it. Every check runs before the launch.
 int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_seq,
@@ -83,8 +105,14 @@ int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_s
               // one (block, head) run must be addressable by a 32-bit offset
               ((int64_t)(block_size - 1) * kt.st + head_size) * 2 < (1ll << 31);
   }
-  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
-                                   (int32_t)width, kv_dtype, aligned);
+  SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
+                             (int32_t)width, kv_dtype, aligned);
+  // Over the link the matrix-core kernel's K tiles (16 token rows of 16 bytes
+  // per lane group) read slower than the VALU kernel's whole rows (measured
+  // on a GQA-4 host tier: 47.9 against 55.9 GB/s; in HBM the two are within
+  // 3 %), so launches that read pinned host memory take the VALU kernel.
+  for (int t = 0; sp.mfma && t < a.ntiers; ++t)
+    if (in_host_memory(a.tier[t].k)) sp.mfma = false;
   const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return set_error(FD_ERR_WORKSPACE,
