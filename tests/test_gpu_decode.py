@@ -321,3 +321,45 @@ def test_row_order_does_not_change_results(gpu, name):
     torch.cuda.synchronize()
     for o, l in res[1:]:
         assert torch.equal(o, res[0][0]) and torch.equal(l, res[0][1])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("D", [128, 256])
+@pytest.mark.parametrize("G", [1, 2, 4, 8])
+def test_kv_adjacent_loads_bit_identical(gpu, dtype, D, G, monkeypatch):
+    """vLLM's cache keeps V right after K in each token row; the VALU kernel
+    then reads a token's K and V in one load and regroups the lanes
+    (v_permlane{16,32}_swap). Same arithmetic in the same order as separate
+    K and V loads (FD_KV_ADJ=0), so the results are bit-identical; both match
+    the oracle. Lengths 0, 1, partial and whole blocks; whole rows and forced
+    2-block splits."""
+    monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    KVH = 2
+    H = G * KVH
+    w = cases.Workload("adj", len(GQA_LENS), H, KVH, D, 16, dtype, 1, 160, 96, D + G)
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    lens[:] = torch.tensor(GQA_LENS, dtype=torch.int32)
+    kc, vc, kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    kv_cpu = kv.cpu()
+    ref_out, ref_lse, st = oracle.decode_attn_f64(q, kv_cpu[..., :D], kv_cpu[..., D:],
+                                                  oracle.VLLM_DIMS, bt, lens, w.scale)
+    assert st == 0
+    nz = lens > 0
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        res = {}
+        for adj in ("1", "0"):
+            monkeypatch.setenv("FD_KV_ADJ", adj)
+            out = torch.empty(w.n, H, D, dtype=torch.float32, device=gpu)
+            o, l = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out=out)
+            o16, _ = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale)
+            torch.cuda.synchronize()
+            res[adj] = (o, l, o16)
+        for a, b in zip(res["1"], res["0"]):
+            assert torch.equal(a, b)
+        o, l, _ = res["1"]
+        assert_out_close(o, ref_out, 2e-3, mask=nz)
+        assert_lse_close(l, ref_lse, mask=nz)
+        assert torch.all(o[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(l[:, ~nz.to(gpu)]))

@@ -161,6 +161,12 @@ def test_fused_equals_monolithic_and_two_partials(gpu, kernel, dtype, H, KVH, mo
                                                       c["full_bt"], c["lens"], c["scale"])
     nz = c["lens"] > 0
     check_vs_oracle(out, lse, ref, ref_lse, nz)
+    # the HBM tier's K + V loads (V after K in vLLM's cache) against separate
+    # K and V loads: bit-identical
+    monkeypatch.setenv("FD_KV_ADJ", "0")
+    out_sep, lse_sep = run_fused(c, gpu)
+    monkeypatch.delenv("FD_KV_ADJ")
+    assert torch.equal(out, out_sep) and torch.equal(lse, lse_sep)
     assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
     merged, mlse = run_two_partials(c, gpu)
     assert float((out - merged)[nz.to(gpu)].abs().max()) <= 2e-5

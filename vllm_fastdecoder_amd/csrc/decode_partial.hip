@@ -150,6 +150,13 @@ int split_blocks_override() {
   return e ? atoi(e) : 0;
 }
 
+// FD_KV_ADJ=0 keeps separate K and V loads where V follows K (comparison and
+// tests).
+bool kv_adj_enabled() {
+  const char* e = getenv("FD_KV_ADJ");
+  return !(e != nullptr && strcmp(e, "0") == 0);
+}
+
 // FD_DECODE_KERNEL=valu keeps grouped-query calls on the VALU kernel
 // (comparison and tests); the matrix-core kernel is the default for G >= 4.
 bool valu_forced() {
@@ -163,9 +170,9 @@ bool valu_forced() {
 // (the reservation is never touched), or 0 when the kernel's own LDS already
 // keeps it there or the reservation would not fit one workgroup's limit.
 // Measured on MI355X: with tasks of 32+ blocks, two workgroups per CU (8
-// waves, one block in flight each) already saturate HBM, and fewer, faster
-// workgroups shorten the drain at the end of the grid (+1 to +6 % over the
-// natural 3-4 per CU); short tasks want the extra workgroups to hide their
+// waves, one block in flight each) already saturate HBM, and the fewer
+// concurrent streams read faster (+1 to +6 % over the natural 3-4 per CU);
+// short tasks want the extra workgroups to hide their
 // start-up latency, so they are left uncapped. `cache` holds the result + 1
 // per device (0 = not computed yet).
 unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache) {
@@ -295,6 +302,12 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     tt.st = kt.st;
     tt.num_blocks = kt.num_blocks;
     tt.run_bytes = (uint32_t)(((int64_t)(kTileTokens - 1) * kt.st + a.D) * 2);
+    // vLLM's cache keeps a token's V right after its K (v == k + D): the VALU
+    // kernel then reads both in one load (tier 0 only; the host tier of a
+    // split keeps separate K and V tensors).
+    tt.kv_adj = t == 0 && (a.D == 128 || a.D == 256) && kv_adj_enabled() &&
+                static_cast<const char*>(kt.v) == static_cast<const char*>(kt.k) + (int64_t)a.D * 2;
+    tt.k_run_bytes = tt.run_bytes + (tt.kv_adj ? (uint32_t)a.D * 2 : 0u);
     tt.bt = kt.bt;
     tt.bt_stride = kt.bt_stride;
     tt.bt_width = kt.bt_width;

@@ -48,7 +48,9 @@ struct TierParams {
   const uint16_t* v;
   int64_t sb, sh, st;  // element strides: block, head, token
   int64_t num_blocks;
-  uint32_t run_bytes;  // extent of one (block, head) run: (15 * st + D) elements
+  uint32_t run_bytes;    // extent of one (block, head) run: (15 * st + D) elements
+  uint32_t k_run_bytes;  // extent of the K resource: run_bytes, or the K + V run if kv_adj
+  bool kv_adj;           // V follows K in every token row (v == k + D): one load reads both
   const int32_t* bt;
   int64_t bt_stride;
   int32_t bt_width;
@@ -124,6 +126,38 @@ __device__ __forceinline__ Vec8 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t o
                                             uint32_t soff = 0) {
   const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kKvLoadPolicy);
   return Vec8{{(uint32_t)u[0], (uint32_t)u[1], (uint32_t)u[2], (uint32_t)u[3]}};
+}
+
+// Loads that read K and V of a token together (a kv_adj tier) leave K and V
+// interleaved in each pair of loads x, y. At D = 128 (16-lane rows, two
+// tokens per load) x = [K a, V a, K b, V b] and y = [K c, V c, K d, V d]; one
+// v_permlane16_swap per dword regroups them into x = [K a, K c, K b, K d] and
+// y = [V a, V c, V b, V d], the layout of separate K and V loads. At D = 256
+// (one token per load) v_permlane32_swap does the same with 32-lane halves:
+// x = [K a, V a], y = [K c, V c] -> x = [K a, K c], y = [V a, V c].
+template <int D>
+__device__ __forceinline__ void split_kv(Vec8& x, Vec8& y) {
+  static_assert(D == 128 || D == 256, "K and V halves of 16 or 32 lanes");
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (D == 128) {
+      const auto r = __builtin_amdgcn_permlane16_swap(x.w[e], y.w[e], false, false);
+      x.w[e] = r[0];
+      y.w[e] = r[1];
+    } else {
+      const auto r = __builtin_amdgcn_permlane32_swap(x.w[e], y.w[e], false, false);
+      x.w[e] = r[0];
+      y.w[e] = r[1];
+    }
+  }
+}
+
+// 16 bytes at `p` through a global load with the non-temporal hint (the
+// same cache policy as kKvLoadPolicy). Callers keep `p` inside the cache.
+__device__ __forceinline__ Vec8 global_ld16(const char* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return Vec8{{u[0], u[1], u[2], u[3]}};
 }
 
 template <typename T>
@@ -353,6 +387,7 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
 // the kernel picks its per-lane offsets for the tier).
 struct BlockSrc {
   __amdgpu_buffer_rsrc_t k, v;
+  const char* kp;  // the K run's first byte (global loads of a kv_adj tier)
   bool t1;
 };
 
@@ -366,8 +401,9 @@ __device__ __forceinline__ BlockSrc block_src(const TiledParams& p, const WaveBl
   const int64_t base = (int64_t)bid * (t1 ? b.sb : a.sb) + (int64_t)kh * (t1 ? b.sh : a.sh);
   const uint32_t rb = t1 ? b.run_bytes : a.run_bytes;
   BlockSrc s;
-  s.k = make_rsrc((t1 ? b.k : a.k) + base, rb);
+  s.k = make_rsrc((t1 ? b.k : a.k) + base, t1 ? b.k_run_bytes : a.k_run_bytes);
   s.v = make_rsrc((t1 ? b.v : a.v) + base, rb);
+  s.kp = reinterpret_cast<const char*>((t1 ? b.k : a.k) + base);
   s.t1 = t1;
   return s;
 }
