@@ -234,7 +234,21 @@ struct V {
   static T add(T a, T b) { return _mm256_add_ps(a, b); }
   static T sub(T a, T b) { return _mm256_sub_ps(a, b); }
   static T mul(T a, T b) { return _mm256_mul_ps(a, b); }
+  static T max(T a, T b) { return _mm256_max_ps(a, b); }
+  static float hmax(T v) {
+    __m128 x = _mm_max_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+    x = _mm_max_ps(x, _mm_movehl_ps(x, x));
+    x = _mm_max_ss(x, _mm_shuffle_ps(x, x, 0x55));
+    return _mm_cvtss_f32(x);
+  }
   static T fma(T a, T b, T c) { return _mm256_fmadd_ps(a, b, c); }
+  // o[0..3] = horizontal sums of a, b, c, d
+  static void hsum4(T a, T b, T c, T d, float* o) {
+    const T ab = _mm256_add_ps(_mm256_unpacklo_ps(a, b), _mm256_unpackhi_ps(a, b));
+    const T cd = _mm256_add_ps(_mm256_unpacklo_ps(c, d), _mm256_unpackhi_ps(c, d));
+    const T s = _mm256_add_ps(_mm256_shuffle_ps(ab, cd, 0x44), _mm256_shuffle_ps(ab, cd, 0xEE));
+    _mm_storeu_ps(o, _mm_add_ps(_mm256_castps256_ps128(s), _mm256_extractf128_ps(s, 1)));
+  }
   static float hsum(T v) {
     __m128 x = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
     x = _mm_add_ps(x, _mm_movehl_ps(x, x));
@@ -290,7 +304,18 @@ struct V512 {
   static T add(T a, T b) { return _mm512_add_ps(a, b); }
   static T sub(T a, T b) { return _mm512_sub_ps(a, b); }
   static T mul(T a, T b) { return _mm512_mul_ps(a, b); }
+  static T max(T a, T b) { return _mm512_max_ps(a, b); }
+  static float hmax(T v) { return _mm512_reduce_max_ps(v); }
   static T fma(T a, T b, T c) { return _mm512_fmadd_ps(a, b, c); }
+  // o[0..3] = horizontal sums of a, b, c, d
+  static void hsum4(T a, T b, T c, T d, float* o) {
+    const T ab = _mm512_add_ps(_mm512_unpacklo_ps(a, b), _mm512_unpackhi_ps(a, b));
+    const T cd = _mm512_add_ps(_mm512_unpacklo_ps(c, d), _mm512_unpackhi_ps(c, d));
+    const T s = _mm512_add_ps(_mm512_shuffle_ps(ab, cd, 0x44), _mm512_shuffle_ps(ab, cd, 0xEE));
+    const __m256 y = _mm256_add_ps(_mm512_castps512_ps256(s),
+                                   _mm256_castpd_ps(_mm512_extractf64x4_pd(_mm512_castps_pd(s), 1)));
+    _mm_storeu_ps(o, _mm_add_ps(_mm256_castps256_ps128(y), _mm256_extractf128_ps(y, 1)));
+  }
   static float hsum(T v) {
     __m256 y = _mm256_add_ps(_mm512_castps512_ps256(v),
                              _mm256_castpd_ps(_mm512_extractf64x4_pd(_mm512_castps_pd(v), 1)));

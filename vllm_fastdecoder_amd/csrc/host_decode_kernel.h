@@ -108,6 +108,92 @@ __attribute__((always_inline)) inline void score_token(const char* kp, const flo
   }
 }
 
+// Scores of TT consecutive tokens (rows kp, kp + st_b, ...) for the G heads:
+// s[g * BS + t], t < TT. The G * TT dot products are independent accumulator
+// chains, reduced four at a time (V::hsum4) instead of one horizontal sum
+// per (head, token).
+template <int DT, int G, int TT>
+__attribute__((always_inline)) inline void score_tokens(const char* kp, int64_t st_b,
+                                                        const float* qf, const uint16_t* qh,
+                                                        float qs, int D, int DW, float* s,
+                                                        int BS) {
+  using T = typename V::T;
+  constexpr int W = V::W;
+  constexpr int elt = DT == FD_F32 ? 4 : 2;
+  static_assert((G * TT) % 4 == 0, "sums are reduced four at a time");
+  alignas(16) float r[G * TT];
+  if constexpr (V::kBf16Dot && DT == FD_BF16) {
+    if (D % 32 == 0) {
+      T c[G][TT];
+#pragma GCC unroll 64
+      for (int j = 0; j < G * TT; ++j) c[j / TT][j % TT] = V::zero();
+      for (int d = 0; d < D; d += 32) {
+        decltype(V::ld_bf16x32(kp)) kv[TT];
+#pragma GCC unroll 16
+        for (int t = 0; t < TT; ++t) kv[t] = V::ld_bf16x32(kp + t * st_b + d * 2);
+#pragma GCC unroll 16
+        for (int g = 0; g < G; ++g) {
+          const auto qv = V::ld_bf16x32(qh + g * D + d);
+#pragma GCC unroll 16
+          for (int t = 0; t < TT; ++t) c[g][t] = V::dot_bf16(c[g][t], qv, kv[t]);
+        }
+      }
+#pragma GCC unroll 64
+      for (int j = 0; j < G * TT; j += 4)
+        V::hsum4(c[j / TT][j % TT], c[(j + 1) / TT][(j + 1) % TT], c[(j + 2) / TT][(j + 2) % TT],
+                 c[(j + 3) / TT][(j + 3) % TT], r + j);
+#pragma GCC unroll 64
+      for (int j = 0; j < G * TT; ++j) s[(j / TT) * BS + j % TT] = r[j] * qs;
+      return;
+    }
+  }
+  constexpr int U = G * TT >= 8 ? 1 : 8 / (G * TT);
+  T c[G][TT][U];
+#pragma GCC unroll 64
+  for (int j = 0; j < G * TT * U; ++j) c[j / (TT * U)][(j / U) % TT][j % U] = V::zero();
+  int d = 0;
+  for (; d + W * U <= DW; d += W * U) {
+#pragma GCC unroll 16
+    for (int u = 0; u < U; ++u) {
+      T kv[TT];
+#pragma GCC unroll 16
+      for (int t = 0; t < TT; ++t) kv[t] = V::template ld<DT>(kp + t * st_b + (d + W * u) * elt);
+#pragma GCC unroll 16
+      for (int g = 0; g < G; ++g) {
+        const T qv = V::load(qf + g * D + d + W * u);
+#pragma GCC unroll 16
+        for (int t = 0; t < TT; ++t) c[g][t][u] = V::fma(qv, kv[t], c[g][t][u]);
+      }
+    }
+  }
+  for (; d < DW; d += W) {
+#pragma GCC unroll 16
+    for (int t = 0; t < TT; ++t) {
+      const T kv = V::template ld<DT>(kp + t * st_b + d * elt);
+#pragma GCC unroll 16
+      for (int g = 0; g < G; ++g) c[g][t][0] = V::fma(V::load(qf + g * D + d), kv, c[g][t][0]);
+    }
+  }
+#pragma GCC unroll 16
+  for (int g = 0; g < G; ++g)
+#pragma GCC unroll 16
+    for (int t = 0; t < TT; ++t)
+#pragma GCC unroll 16
+      for (int step = 1; step < U; step *= 2)
+#pragma GCC unroll 16
+        for (int u = 0; u + step < U; u += 2 * step) c[g][t][u] = V::add(c[g][t][u], c[g][t][u + step]);
+#pragma GCC unroll 64
+  for (int j = 0; j < G * TT; j += 4)
+    V::hsum4(c[j / TT][j % TT][0], c[(j + 1) / TT][(j + 1) % TT][0],
+             c[(j + 2) / TT][(j + 2) % TT][0], c[(j + 3) / TT][(j + 3) % TT][0], r + j);
+  for (int j = 0; j < G * TT; ++j) {
+    const int g = j / TT, t = j % TT;
+    float sc = r[j];
+    for (int e = DW; e < D; ++e) sc += qf[g * D + e] * load1(kp + t * st_b, e, DT);
+    s[g * BS + t] = sc;
+  }
+}
+
 // Online-softmax partial of query heads kh*Gr + g0 .. + G-1 (Gr = H / KVH) of
 // sequence i over kv head kh. Returns false if the row is invalid (a length
 // past its table or a block id outside the cache).
@@ -118,6 +204,8 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
   constexpr int elt = DT == FD_F32 ? 4 : 2;
   constexpr int U = G >= 8 ? 1 : 8 / G;   // score chains per head (>= 8 in all)
   constexpr int CU = G >= V::kAcc ? 1 : V::kAcc / G;  // P.V chunks in flight
+  constexpr int TT0 = V::kAcc / G < 4 ? V::kAcc / G : 4;  // tokens scored together
+  constexpr int TT = (G * TT0) % 4 == 0 ? TT0 : 1;
   const int D = a.D, BS = a.BS, Gr = a.H / a.KVH;
   const int DW = D - D % W;
   const int L = a.lens[i];
@@ -167,15 +255,29 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
           }
       }
     }
-    // scores
-    for (int t = 0; t < ntok; ++t)
+    // scores, TT tokens at a time where the accumulators fit
+    int t0 = 0;
+    if constexpr (TT >= 2) {
+      for (; t0 + TT <= ntok; t0 += TT)
+        score_tokens<DT, G, TT>(kbase + (base + (int64_t)t0 * a.st) * elt, a.st * elt, qf, qh,
+                                qs, D, DW, s + t0, BS);
+    }
+    for (int t = t0; t < ntok; ++t)
       score_token<DT, G, U>(kbase + (base + (int64_t)t * a.st) * elt, qf, qh, qs, D, DW, s + t,
                             BS);
     // one online-softmax step per head
     for (int g = 0; g < G; ++g) {
       float* sg = s + g * BS;
-      float bmax = sg[0];
-      for (int t = 1; t < ntok; ++t) bmax = std::max(bmax, sg[t]);
+      float bmax = -INFINITY;
+      {
+        int t = 0;
+        if (ntok >= W) {
+          T mx = V::load(sg);
+          for (t = W; t + W <= ntok; t += W) mx = V::max(mx, V::load(sg + t));
+          bmax = V::hmax(mx);
+        }
+        for (; t < ntok; ++t) bmax = std::max(bmax, sg[t]);
+      }
       const float mn = std::max(m[g], bmax);
       alpha[g] = m[g] == -INFINITY ? 0.f : V::exp2_1(m[g] - mn);
       const T mv = V::set1(mn);
