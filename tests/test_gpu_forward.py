@@ -18,7 +18,6 @@ from types import SimpleNamespace
 import pytest
 import torch
 
-import oracle
 from tests.test_plan import KATS, scenario
 from vllm_fastdecoder_amd import backend, plan, state
 from vllm_fastdecoder_amd.pinned import pinned_zeros

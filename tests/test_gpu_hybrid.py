@@ -181,3 +181,21 @@ def test_two_micro_batches_interleaved_with_other_gpu_work(gpu):
     for c, (out, lse) in zip((ca, cb), outs):
         ref_o, ref_l = oracle_merged(c)
         check(out, lse, ref_o, ref_l, c["lens"])
+
+
+def test_hybrid_with_device_hbm_tables(gpu):
+    """The HBM tier's table and lengths already on the GPU (no host-side row
+    order then) give the oracle's result, as do host copies of them."""
+    c = two_tier_case(10, 16, 4, 128, torch.float16, seed=31, dev=gpu)
+    ref_o, ref_l = oracle_merged(c)
+    q = c["q"].to(gpu)
+    n, H, D = q.shape
+    for dev_tables in (True, False):
+        bt_g = c["bt_g"].to(gpu) if dev_tables else c["bt_g"]
+        len_g = c["len_g"].to(gpu) if dev_tables else c["len_g"]
+        out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+        ops.hybrid_split_decode(q, c["kv"][..., :D], c["kv"][..., D:], bt_g, len_g, c["hk"],
+                                c["hv"], c["bt_c"], c["len_c"], c["scale"], 0.5, out=out, lse=lse)
+        torch.cuda.synchronize()
+        check(out, lse, ref_o, ref_l, c["lens"])

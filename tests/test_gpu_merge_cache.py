@@ -15,7 +15,6 @@ import pytest
 import torch
 
 import oracle
-from tests import cases
 from vllm_fastdecoder_amd import ops
 from vllm_fastdecoder_amd.pinned import pinned_zeros
 

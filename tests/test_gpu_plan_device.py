@@ -14,7 +14,6 @@ exactly with
 
 from __future__ import annotations
 
-import math
 import random
 from types import SimpleNamespace
 

@@ -417,7 +417,7 @@ def hybrid_split_begin(
             return HYBRID_STAGING.upload(idx, name, t, dev)
 
         # rows by decreasing GPU work when the HBM lengths are known on the host
-            order = None
+        order = None
         if not hbm_lens.is_cuda:
             work = hbm_lens.numpy().astype(np.int64) + share.gpu_lens.numpy()
             order = up("order", torch.from_numpy(
