@@ -199,3 +199,24 @@ def test_hybrid_with_device_hbm_tables(gpu):
                                 c["hv"], c["bt_c"], c["len_c"], c["scale"], 0.5, out=out, lse=lse)
         torch.cuda.synchronize()
         check(out, lse, ref_o, ref_l, c["lens"])
+
+
+def test_cancel_frees_the_device_for_the_next_split(gpu):
+    """A split abandoned between begin and finish (the caller's step failed)
+    is cancelled: the next begin on the device is accepted and correct;
+    cancel after finish is a no-op."""
+    c = two_tier_case(6, 8, 2, 64, torch.float16, seed=41, dev=gpu)
+    q = c["q"].to(gpu)
+    n, H, D = q.shape
+    args = (q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"], c["hk"], c["hv"],
+            c["bt_c"], c["len_c"], c["scale"], 0.5)
+    h = ops.hybrid_split_begin(*args)
+    h.cancel()
+    out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    h2 = ops.hybrid_split_begin(*args, out=out, lse=lse)
+    h2.finish()
+    h2.cancel()
+    torch.cuda.synchronize()
+    ref_o, ref_l = oracle_merged(c)
+    check(out, lse, ref_o, ref_l, c["lens"])

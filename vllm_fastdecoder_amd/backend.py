@@ -301,8 +301,31 @@ class SplitDecodeImpl:
             ops.decode_attn(qs, k_host, v_host, dp.s_cpu_bt, dp.s_cpu_lens, float(self.scale),
                             o_cpu, lse_cpu, row_order=dp.s_cpu_order)
 
-        # 3) attention that touches no host block: P (all-HBM requests) and F
-        #    (fresh prefills over this step's q/k/v) -- prefill forms of OPS.fa
+        try:
+            self._prefill_rows(query, key, value, key_cache, value_cache, dp, output)
+        except BaseException:
+            if hybrid is not None:  # free the staging of the split begun above
+                hybrid.cancel()
+            raise
+
+        # 4) merge the split decodes' partials into their output rows
+        if hybrid is not None:
+            merged, _ = hybrid.finish()
+            if self._tuner is not None:
+                self._tuner.update(hybrid.gpu_finished_first)
+        if ns:
+            if not fused:
+                merged = torch.empty_like(qs)
+                OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
+            output.index_copy_(0, dp.s_tok, merged)
+        return output
+
+    def _prefill_rows(self, query, key, value, key_cache, value_cache, dp: DevicePlan, output):
+        """Step 3 of _forward_split: attention that touches no host block, P
+        (all-HBM requests) and F (fresh prefills over this step's q/k/v), by
+        the prefill forms of OPS.fa."""
+        hp = dp.host
+        fa = OPS.fa
         if hp.n_p_tok:
             q_p = query.index_select(0, dp.p_tok)
             o_p = fa(
@@ -321,18 +344,6 @@ class SplitDecodeImpl:
                 causal=True, softcap=self.logits_soft_cap,
             )
             output.index_copy_(0, dp.f_tok, o_f)
-
-        # 4) merge the split decodes' partials into their output rows
-        if hybrid is not None:
-            merged, _ = hybrid.finish()
-            if self._tuner is not None:
-                self._tuner.update(hybrid.gpu_finished_first)
-        if ns:
-            if not fused:
-                merged = torch.empty_like(qs)
-                OPS.merge(merged, o_gpu, lse_gpu, o_cpu, lse_cpu)
-            output.index_copy_(0, dp.s_tok, merged)
-        return output
 
     def _forward_device(self, layer, query, key, value, kv_cache, ds: DeviceStep, output):
         """The step of _forward_split planned on the GPU (build_device_step):
@@ -381,16 +392,21 @@ class SplitDecodeImpl:
                 output.index_copy_(0, ds.dec_tok, out)
 
         # 3) fresh prefills attend only this step's q/k/v (backend.py:331-340)
-        if ds.n_f_tok:
-            q_f = query.index_select(0, ds.f_tok)
-            k_f = key.index_select(0, ds.f_tok)
-            v_f = value.index_select(0, ds.f_tok)
-            o_f = OPS.fa(
-                q=q_f, k=k_f, v=v_f, cu_seqlens_q=ds.f_cu, cu_seqlens_k=ds.f_cu,
-                max_seqlen_q=ds.f_max, max_seqlen_k=ds.f_max, softmax_scale=self.scale,
-                causal=True, softcap=self.logits_soft_cap,
-            )
-            output.index_copy_(0, ds.f_tok, o_f)
+        try:
+            if ds.n_f_tok:
+                q_f = query.index_select(0, ds.f_tok)
+                k_f = key.index_select(0, ds.f_tok)
+                v_f = value.index_select(0, ds.f_tok)
+                o_f = OPS.fa(
+                    q=q_f, k=k_f, v=v_f, cu_seqlens_q=ds.f_cu, cu_seqlens_k=ds.f_cu,
+                    max_seqlen_q=ds.f_max, max_seqlen_k=ds.f_max, softmax_scale=self.scale,
+                    causal=True, softcap=self.logits_soft_cap,
+                )
+                output.index_copy_(0, ds.f_tok, o_f)
+        except BaseException:
+            if hybrid is not None:  # free the staging of the split begun above
+                hybrid.cancel()
+            raise
         if hybrid is not None:  # the host cores' share, while the GPU runs the above
             out, _ = hybrid.finish()
             if self._tuner is not None:

@@ -337,6 +337,15 @@ class HybridSplit:
         # finished (None before finish): the signal that balances the share
         self.gpu_finished_first: bool | None = None
 
+    def cancel(self) -> None:
+        """Abandons a split that will not be finished (the caller's step
+        failed between begin and finish): frees the device's staging for the
+        next split and leaves out / lse unwritten. No-op after finish()."""
+        if self._o_gpu is None:
+            return
+        HYBRID_STAGING.release(self._staging_idx, torch.cuda.current_stream(self.out.device))
+        self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
+
     def finish(self) -> tuple[torch.Tensor, torch.Tensor]:
         """Waits for q on the host, reduces the host cores' blocks (blocking
         the caller), uploads that partial and enqueues the merge."""
