@@ -18,13 +18,16 @@ Every step runs twice on the same q/k/v:
 Both start from different random garbage, so any read of an unwritten slot
 shows. Checked per step: every decode row of the split path against the
 monolithic output; every slot written this step bit-exact in its tier; every
-`oracle_every` steps a few rows against the float64 oracle.
+`oracle_every` steps a few rows against the float64 oracle. Reported besides:
+the split path's wall time per step (planning, KV writes and attention, with
+the prefill rows' attention stubbed as below), `split_path_ms`.
 """
 
 from __future__ import annotations
 
 import math
 import random
+import time
 from types import SimpleNamespace
 
 import numpy as np
@@ -117,6 +120,7 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
              "host_tokens": 0, "max_err_vs_mono": 0.0, "max_err_vs_f64": 0.0, "dropped": 0,
              "device_planned_steps": 0}
     plan_errors = torch.zeros(1, dtype=torch.int32, device=dev)
+    step_ms = []
     try:
         for step in range(steps):
             rows = []
@@ -169,8 +173,10 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
             v = v.view(Tp, KVH, D)
             bt_d, slots_d = bt.to(dev), slots.to(dev)
 
-            # ---- split path
+            # ---- split path (timed from planning to its last kernel)
             out_split = torch.full((Tp, H, D), float("nan"), dtype=dtype, device=dev)
+            torch.cuda.synchronize(dev)
+            t_split = time.perf_counter()
             ds = (backend.build_device_step(qsl, seq, bt_d, slots_d, R, store, dev)
                   if planner == "device" else None)
             dp = backend.build_split_plan(qsl, seq, bt_d, slots_d, R, store, dev) \
@@ -193,6 +199,9 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                 stats["split_rows"] += dp.host.n_s
                 stats["host_tokens"] += int(dp.host.s_cpu_lens.sum())
                 impl._forward_split(layer, q, k, v, kv_cache, dp, out_split)
+
+            torch.cuda.synchronize(dev)
+            step_ms.append((time.perf_counter() - t_split) * 1e3)
 
             # ---- monolithic path: same writes into one pool, fp32 decode
             ops.reshape_and_cache(k, v, ukc, uvc, slots_d)
@@ -248,6 +257,11 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                     running.remove(r)
                     release(r["blocks"])
         torch.cuda.synchronize()
+        if step_ms:  # wall time of the split path per step (planning, KV writes, attention)
+            t = np.array(step_ms[10:] or step_ms)  # the first steps warm up
+            stats["split_path_ms"] = {"median": round(float(np.median(t)), 3),
+                                      "mean": round(float(t.mean()), 3),
+                                      "p90": round(float(np.percentile(t, 90)), 3)}
         if int(plan_errors.item()):
             stats["failures"].append(f"device planner counted {int(plan_errors.item())} errors")
     finally:
