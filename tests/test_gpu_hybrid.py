@@ -220,3 +220,19 @@ def test_cancel_frees_the_device_for_the_next_split(gpu):
     torch.cuda.synchronize()
     ref_o, ref_l = oracle_merged(c)
     check(out, lse, ref_o, ref_l, c["lens"])
+
+
+def test_failed_begin_leaves_the_device_usable(gpu):
+    """begin raising part-way (here: an HBM table of the wrong dtype, refused
+    by the GPU launch's checks after q's copy to the host was enqueued) frees
+    the staging and re-raises; the next split is correct."""
+    c = two_tier_case(6, 8, 2, 64, torch.float16, seed=43, dev=gpu)
+    q = c["q"].to(gpu)
+    n, H, D = q.shape
+    with pytest.raises(RuntimeError, match="int32"):
+        ops.hybrid_split_begin(q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"].long(),
+                               c["len_g"], c["hk"], c["hv"], c["bt_c"], c["len_c"], c["scale"],
+                               0.5)
+    out, lse = run_hybrid(c, gpu, 0.5)
+    ref_o, ref_l = oracle_merged(c)
+    check(out, lse, ref_o, ref_l, c["lens"])

@@ -318,60 +318,86 @@ class _HybridStaging:
 HYBRID_STAGING = _HybridStaging()
 
 
+class _HostShareRunner:
+    """One background thread per process that runs the host cores' share of
+    hybrid splits (the host-core kernel releases the GIL), so the share starts
+    as soon as q reaches the host rather than when the caller calls finish().
+    Recreated in a forked child, where the parent's thread does not exist."""
+
+    def __init__(self) -> None:
+        self._lock = threading.Lock()
+        self._pid = None
+        self._ex = None
+
+    def submit(self, fn):
+        import concurrent.futures
+        import os
+
+        with self._lock:
+            if self._ex is None or self._pid != os.getpid():
+                self._ex = concurrent.futures.ThreadPoolExecutor(
+                    max_workers=1, thread_name_prefix="fd-host-share")
+                self._pid = os.getpid()
+            return self._ex.submit(fn)
+
+
+_HOST_SHARE = _HostShareRunner()
+
+
 class HybridSplit:
     """A hybrid split decode in flight (hybrid_split_begin): the GPU's share
-    is enqueued; finish() runs the host cores' share and enqueues the merge."""
+    is enqueued and the host cores' share runs in the background; finish()
+    waits for the latter and enqueues the merge."""
 
-    def __init__(self, out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
-                 host_v_cache, share, softmax_scale, num_threads, staging_idx=None):
+    def __init__(self, out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_fn=None, host_job=None,
+                 staging_idx=None):
         self.out, self.lse = out, lse
         self._staging_idx = staging_idx
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
-        self._q_host, self._q_ready, self._gpu_done = q_host, q_ready, gpu_done
-        self._hk, self._hv = host_k_cache, host_v_cache
-        self._share = share
-        self._scale = softmax_scale
-        self._threads = num_threads
+        self._o_cpu, self._l_cpu = o_cpu, l_cpu
+        # the host cores' share, and its future on the background thread; both
+        # give (host seconds, whether the GPU's launch was done at its end)
+        self._fn, self._job = host_fn, host_job
         self.cpu_seconds = 0.0  # wall time of the host cores' share (0 before finish)
         # whether the GPU's fused launch had completed when the host cores
         # finished (None before finish): the signal that balances the share
         self.gpu_finished_first: bool | None = None
 
+    def _drop(self) -> None:
+        HYBRID_STAGING.release(self._staging_idx, torch.cuda.current_stream(self.out.device))
+        self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._job = self._fn = None
+
     def cancel(self) -> None:
         """Abandons a split that will not be finished (the caller's step
-        failed between begin and finish): frees the device's staging for the
-        next split and leaves out / lse unwritten. No-op after finish()."""
+        failed between begin and finish): waits for the host cores' share to
+        stop using the staging, frees it for the next split and leaves out /
+        lse unwritten. No-op after finish()."""
         if self._o_gpu is None:
             return
-        HYBRID_STAGING.release(self._staging_idx, torch.cuda.current_stream(self.out.device))
-        self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
+        try:
+            if not self._job.cancel():  # already running: wait, whatever its outcome
+                self._job.exception()
+        finally:
+            self._drop()
 
     def finish(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """Waits for q on the host, reduces the host cores' blocks (blocking
-        the caller), uploads that partial and enqueues the merge."""
+        """Waits for the host cores' share, uploads that partial and enqueues
+        the merge."""
         if self._o_gpu is None:
             return self.out, self.lse
-        import time
-
         dev = self.out.device
-        n, H, D = self.out.shape
-        idx = self._staging_idx
         try:
-            o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
-            l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
-            self._q_ready.synchronize()
-            t0 = time.perf_counter()
-            host_decode_attn(self._q_host, self._hk, self._hv, self._share.cpu_bt,
-                             self._share.cpu_lens, self._scale, o_cpu, l_cpu,
-                             num_threads=self._threads)
-            self.cpu_seconds = time.perf_counter() - t0
-            self.gpu_finished_first = bool(self._gpu_done.query())
+            # not picked up by the background thread yet: run it here instead
+            # (saves the thread hand-off when finish follows begin at once)
+            res = self._fn() if self._job.cancel() else self._job.result()
+            self.cpu_seconds, self.gpu_finished_first = res
             merge_attn_states(self.out, self._o_gpu, self._l_gpu,
-                              o_cpu.to(dev, non_blocking=True), l_cpu.to(dev, non_blocking=True),
-                              out_lse=self.lse)
+                              self._o_cpu.to(dev, non_blocking=True),
+                              self._l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
         finally:
-            HYBRID_STAGING.release(idx, torch.cuda.current_stream(dev))
-            self._o_gpu = self._l_gpu = self._q_host = self._gpu_done = None
+            if self._job is not None and not self._job.done():
+                self._job.exception()  # finish interrupted: let the share stop first
+            self._drop()
         return self.out, self.lse
 
 
@@ -394,8 +420,10 @@ def hybrid_split_begin(
     host_block_table_dev: torch.Tensor | None = None,
 ) -> HybridSplit:
     """First half of hybrid_split_decode: divides the host tier, starts the
-    copy of q to the host and enqueues the GPU's fused launch. Other GPU work
-    can be enqueued before HybridSplit.finish(). hbm_lens_dev /
+    copy of q to the host, enqueues the GPU's fused launch and then starts the
+    host cores' share on a background thread. Other GPU work can be enqueued
+    before HybridSplit.finish(), which waits for the host cores and enqueues
+    the merge. hbm_lens_dev /
     host_block_table_dev: device copies of hbm_lens / host_block_table the
     caller already holds (the GPU's share reads the host table unchanged,
     only with shorter lengths), saving their uploads."""
@@ -412,8 +440,7 @@ def hybrid_split_begin(
         lse = torch.empty(H, n, dtype=torch.float32, device=dev)
     share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
     if n == 0:
-        return HybridSplit(out, lse, None, None, None, None, None, host_k_cache, host_v_cache,
-                           share, softmax_scale, num_threads)
+        return HybridSplit(out, lse, None, None, None, None, None)
     stream = torch.cuda.current_stream(dev)
     idx = HYBRID_STAGING.acquire(dev)
     try:
@@ -439,13 +466,28 @@ def hybrid_split_begin(
         split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table), hl,
                      host_k_cache, host_v_cache, hbt, up("gpu_lens", share.gpu_lens),
                      softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
+        gpu_done = torch.cuda.Event()
+        gpu_done.record(stream)
+        o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
+        l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
+
+        def host_share():  # the host cores' blocks, from when q is on the host
+            import time
+
+            q_ready.synchronize()
+            t0 = time.perf_counter()
+            host_decode_attn(q_host, host_k_cache, host_v_cache, share.cpu_bt, share.cpu_lens,
+                             softmax_scale, o_cpu, l_cpu, num_threads=num_threads)
+            return time.perf_counter() - t0, bool(gpu_done.query())
+
+        # submitted after the GPU's launch: the share's threads take every
+        # host core, and the launch path above would otherwise compete with
+        # them (measured slower when the GPU side bounds the step)
+        job = _HOST_SHARE.submit(host_share)
     except BaseException:
         HYBRID_STAGING.release(idx, stream)
         raise
-    gpu_done = torch.cuda.Event()
-    gpu_done.record(stream)
-    return HybridSplit(out, lse, o_gpu, l_gpu, q_host, q_ready, gpu_done, host_k_cache,
-                       host_v_cache, share, softmax_scale, num_threads, staging_idx=idx)
+    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_share, job, staging_idx=idx)
 
 
 def hybrid_split_decode(
