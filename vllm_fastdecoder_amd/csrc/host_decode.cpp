@@ -235,6 +235,12 @@ struct V {
   static T sub(T a, T b) { return _mm256_sub_ps(a, b); }
   static T mul(T a, T b) { return _mm256_mul_ps(a, b); }
   static T max(T a, T b) { return _mm256_max_ps(a, b); }
+  // 2W bf16 at p as fp32: even-indexed elements in `ev`, odd in `od`
+  static void ld_bf16_eo(const void* p, T& ev, T& od) {
+    const __m256i x = _mm256_loadu_si256(static_cast<const __m256i*>(p));
+    ev = _mm256_castsi256_ps(_mm256_slli_epi32(x, 16));
+    od = _mm256_castsi256_ps(_mm256_and_si256(x, _mm256_set1_epi32((int)0xFFFF0000u)));
+  }
   static float hmax(T v) {
     __m128 x = _mm_max_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
     x = _mm_max_ps(x, _mm_movehl_ps(x, x));
@@ -305,6 +311,12 @@ struct V512 {
   static T sub(T a, T b) { return _mm512_sub_ps(a, b); }
   static T mul(T a, T b) { return _mm512_mul_ps(a, b); }
   static T max(T a, T b) { return _mm512_max_ps(a, b); }
+  // 2W bf16 at p as fp32: even-indexed elements in `ev`, odd in `od`
+  static void ld_bf16_eo(const void* p, T& ev, T& od) {
+    const __m512i x = _mm512_loadu_si512(p);
+    ev = _mm512_castsi512_ps(_mm512_slli_epi32(x, 16));
+    od = _mm512_castsi512_ps(_mm512_and_si512(x, _mm512_set1_epi32((int)0xFFFF0000u)));
+  }
   static float hmax(T v) { return _mm512_reduce_max_ps(v); }
   static T fma(T a, T b, T c) { return _mm512_fmadd_ps(a, b, c); }
   // o[0..3] = horizontal sums of a, b, c, d

@@ -11,7 +11,11 @@
 // acc[g][d0 .. d0 + W*CU) = acc * alpha[g] + sum_t s[g][t] * V[t][...] for as
 // many whole groups of CU chunks as fit below DW, advancing d; the rest goes
 // to groups of CU / 2, and so on. The G*CU accumulators stay in registers.
-template <int DT, int G, int CU>
+// PERM (bf16 V): each 2W-element load is split into its even- and
+// odd-indexed elements by one shift and one mask, so acc holds every 2W span
+// as [even elements, odd elements]; run_heads restores the order at the end.
+// The same products in the same order: results equal the plain layout's.
+template <int DT, int G, int CU, bool PERM = false>
 __attribute__((always_inline)) inline void pv_groups(float* acc, const float* s, const float* alpha, const char* vb,
                       int64_t st, int D, int DW, int BS, int ntok, int& d) {
   using T = typename V::T;
@@ -26,15 +30,26 @@ __attribute__((always_inline)) inline void pv_groups(float* acc, const float* s,
       const char* vp = vb + (int64_t)t * st * elt;
       T p[G];
       for (int g = 0; g < G; ++g) p[g] = V::bcast(s + g * BS + t);
-      for (int u = 0; u < CU; ++u) {
-        const T vv = V::template ld<DT>(vp + (d + W * u) * elt);
-        for (int g = 0; g < G; ++g) r[g][u] = V::fma(p[g], vv, r[g][u]);
+      if constexpr (PERM && CU % 2 == 0) {
+        for (int u = 0; u < CU; u += 2) {
+          T ev, od;
+          V::ld_bf16_eo(vp + (d + W * u) * elt, ev, od);
+          for (int g = 0; g < G; ++g) {
+            r[g][u] = V::fma(p[g], ev, r[g][u]);
+            r[g][u + 1] = V::fma(p[g], od, r[g][u + 1]);
+          }
+        }
+      } else {
+        for (int u = 0; u < CU; ++u) {
+          const T vv = V::template ld<DT>(vp + (d + W * u) * elt);
+          for (int g = 0; g < G; ++g) r[g][u] = V::fma(p[g], vv, r[g][u]);
+        }
       }
     }
     for (int g = 0; g < G; ++g)
       for (int u = 0; u < CU; ++u) V::store(acc + g * D + d + W * u, r[g][u]);
   }
-  if constexpr (CU > 1) pv_groups<DT, G, CU / 2>(acc, s, alpha, vb, st, D, DW, BS, ntok, d);
+  if constexpr (CU > 1) pv_groups<DT, G, CU / 2, PERM>(acc, s, alpha, vb, st, D, DW, BS, ntok, d);
 }
 
 // s[g * BS] = q[g] . K row at kp for the G heads, with U independent
@@ -208,6 +223,10 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
   constexpr int TT = (G * TT0) % 4 == 0 ? TT0 : 1;
   const int D = a.D, BS = a.BS, Gr = a.H / a.KVH;
   const int DW = D - D % W;
+  // bf16 V: P.V on even / odd halves of 2W-element loads (D a multiple of 2W,
+  // and each P.V group an even number of W chunks: CU >= 2 at every level)
+  constexpr bool kPermOk = DT == FD_BF16 && CU >= 2;
+  const bool perm = kPermOk && D % (2 * W) == 0 && (D / W) % 2 == 0;
   const int L = a.lens[i];
   const int nb = (L + BS - 1) / BS;
   if (nb > a.bt_width) return false;
@@ -300,7 +319,10 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
     // halving groups for what is left
     const char* vb = vbase + base * elt;
     int d = 0;
-    pv_groups<DT, G, CU>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
+    if (perm)
+      pv_groups<DT, G, CU, true>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
+    else
+      pv_groups<DT, G, CU>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
     for (; d < D; ++d)
       for (int g = 0; g < G; ++g) {
         float x = acc[g * D + d] * alpha[g];
@@ -312,6 +334,16 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
     const int h = kh * Gr + g0 + g;
     const float inv = 1.f / l[g];
     float* o = acc + g * D;
+    if (perm) {  // back from the even / odd layout of each 2W span
+      float tmp[2 * W];
+      for (int d0 = 0; d0 < D; d0 += 2 * W) {
+        for (int j = 0; j < W; ++j) {
+          tmp[2 * j] = o[d0 + j];
+          tmp[2 * j + 1] = o[d0 + W + j];
+        }
+        memcpy(o + d0, tmp, sizeof(tmp));
+      }
+    }
     for (int d = 0; d < D; ++d) o[d] *= inv;
     const int64_t ob = (int64_t)i * a.out_ss + (int64_t)h * a.out_sh;
     if (a.out_dt == FD_F32) {
