@@ -363,3 +363,87 @@ def test_kv_adjacent_loads_bit_identical(gpu, dtype, D, G, monkeypatch):
         assert_lse_close(l, ref_lse, mask=nz)
         assert torch.all(o[~nz.to(gpu)] == 0)
         assert torch.all(torch.isneginf(l[:, ~nz.to(gpu)]))
+
+
+@pytest.mark.parametrize("kernel", ["default", "valu"])
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 32, torch.float16), (32, 8, torch.bfloat16)])
+def test_long_rows_split_by_the_model_match_oracle(gpu, kernel, H, KVH, dtype, monkeypatch):
+    """Rows far past one task (16k+ tokens = 1025 blocks; a task holds at most
+    256) in vLLM's layout: the launch-time model picks the task size, rows
+    split and the combine kernel merges them. Also a 5000-token row, a short
+    one and an empty one in the same launch."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    D, BS = 128, 16
+    lens = torch.tensor([16384 + 7, 5000, 0, 300], dtype=torch.int32)
+    w = cases.Workload("long", len(lens), H, KVH, D, BS, dtype, 1, int(lens.max()), None, 7)
+    nb = (lens + BS - 1) // BS
+    pool = int(nb.sum())
+    W = int(nb.max())
+    g = torch.Generator().manual_seed(7)
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    bt = torch.zeros(w.n, W, dtype=torch.int32)
+    pos = 0
+    for i in range(w.n):
+        bt[i, : int(nb[i])] = perm[pos: pos + int(nb[i])]
+        pos += int(nb[i])
+    kc, vc, kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    out = torch.empty(w.n, H, D, dtype=torch.float32, device=gpu)
+    o, l = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out=out)
+    torch.cuda.synchronize()
+    kv_cpu = kv.cpu()
+    ref_out, ref_lse, st = oracle.decode_attn_f64(q, kv_cpu[..., :D], kv_cpu[..., D:],
+                                                  oracle.VLLM_DIMS, bt, lens, w.scale)
+    assert st == 0
+    nz = lens > 0
+    assert_out_close(o, ref_out, 2e-3, mask=nz)
+    assert_lse_close(l, ref_lse, mask=nz)
+    assert torch.all(o[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(l[:, ~nz.to(gpu)]))
+
+
+def test_block_offsets_past_4gib(gpu):
+    """A 4.4 GiB vLLM cache (MHA fp16, 256 KiB per block): rows whose blocks sit
+    at the far end of the pool read at byte offsets beyond 2^32 from the base,
+    checked against the oracle on the gathered blocks."""
+    H = KVH = 32
+    D, BS, dtype = 128, 16, torch.float16
+    num_blocks = 18000  # 18000 * 16 * 32 * 256 * 2 B = 4.4 GiB
+    phys = torch.empty(num_blocks, BS, KVH, 2 * D, dtype=dtype, device=gpu)
+    lens = torch.tensor([700, 33, 1024, 0, 17], dtype=torch.int32)
+    nb = (lens + BS - 1) // BS
+    W = int(nb.max())
+    g = torch.Generator().manual_seed(5)
+    # high ids (past 2^32 bytes from the base: block >= 16385) plus a few low ones
+    ids = torch.cat([torch.randperm(num_blocks - 16400, generator=g)[:150] + 16400,
+                     torch.randperm(100, generator=g)[:20]]).to(torch.int32)
+    ids = ids[torch.randperm(len(ids), generator=g)]
+    bt = torch.zeros(len(lens), W, dtype=torch.int32)
+    pos = 0
+    for i in range(len(lens)):
+        k = int(nb[i])
+        bt[i, :k] = ids[pos: pos + k]
+        pos += k
+    used = torch.unique(bt[bt > 0].long())
+    gk = torch.Generator(device=gpu).manual_seed(9)
+    phys[used.to(gpu)] = torch.randn(len(used), BS, KVH, 2 * D, generator=gk, device=gpu).to(dtype)
+    phys[0] = torch.randn(BS, KVH, 2 * D, generator=gk, device=gpu).to(dtype)  # pad id 0 is read too
+    q = torch.randn(len(lens), H, D, generator=torch.Generator().manual_seed(3)).to(dtype).to(gpu)
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty(len(lens), H, D, dtype=torch.float32, device=gpu)
+    o, l = ops.paged_decode(q, phys[..., :D], phys[..., D:], bt.to(gpu), lens.to(gpu), scale,
+                            out=out)
+    torch.cuda.synchronize()
+    # the oracle on the gathered blocks (ids remapped to their position)
+    keep = torch.cat([torch.zeros(1, dtype=torch.long), used])
+    remap = torch.zeros(num_blocks, dtype=torch.int32)
+    remap[keep] = torch.arange(len(keep), dtype=torch.int32)
+    small = phys[keep.to(gpu)].cpu()
+    ref_out, ref_lse, st = oracle.decode_attn_f64(q, small[..., :D], small[..., D:],
+                                                  oracle.VLLM_DIMS, remap[bt.long()], lens, scale)
+    assert st == 0
+    nz = lens > 0
+    assert_out_close(o, ref_out, 2e-3, mask=nz)
+    assert_lse_close(l, ref_lse, mask=nz)
+    del phys
+    torch.cuda.empty_cache()
