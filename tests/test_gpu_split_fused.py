@@ -268,3 +268,20 @@ def test_fused_second_tier_in_hbm(gpu, dtype):
     check_vs_oracle(out, lse, ref, ref_lse, nz)
     out_h, lse_h = run_fused(c, gpu)  # the same step reading the pinned host tier
     assert float((out - out_h)[nz.to(gpu)].abs().max()) <= 2e-5
+
+
+@pytest.mark.parametrize("kernel", ["default", "valu"])
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 32, torch.float16), (32, 8, torch.bfloat16)])
+def test_fused_long_rows(gpu, kernel, H, KVH, dtype, monkeypatch):
+    """Rows of 6k-9k tokens (375-563 blocks, past one 256-block task) with
+    their blocks divided at random between the tiers: the launch model's
+    splits cross the tier boundary and the combine kernel merges them."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    c = two_tier_case(5, H, KVH, 128, dtype, seed=H + KVH + 1, dev=gpu, G=2000, C=2600,
+                      lo=6000, hi=9000)
+    out, lse = run_fused(c, gpu)
+    ref, ref_lse = oracle_merged(c)
+    nz = c["lens"] > 0
+    check_vs_oracle(out, lse, ref, ref_lse, nz)
+    assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
