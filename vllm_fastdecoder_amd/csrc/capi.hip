@@ -49,8 +49,9 @@ bool in_host_memory(const void* p) {
   for (const Entry& e : cache)
     if (e.p == p) return e.host;
   hipPointerAttribute_t attr{};
-  const bool host = hipPointerGetAttributes(&attr, p) == hipSuccess && attr.type == hipMemoryTypeHost;
-  (void)hipGetLastError();  // a pointer the runtime does not know leaves no error behind
+  const hipError_t rc = hipPointerGetAttributes(&attr, p);
+  if (rc != hipSuccess) (void)hipGetLastError();  // an unknown pointer leaves no error behind
+  const bool host = rc == hipSuccess && attr.type == hipMemoryTypeHost;
   cache[next] = {p, host};
   next = (next + 1) % kEntries;
   return host;
