@@ -303,7 +303,8 @@ int fd_host_device_pointer(void* host_ptr, void** device_ptr);
  * fd_paged_decode_partial -- except that every pointer is a HOST address
  * (q, caches, table, lengths, out, lse) and the call runs synchronously on
  * the calling thread plus a persistent pool of num_threads - 1 workers
- * (0: one per CPU of the process's affinity mask, or FASTDECODE_CPU_THREADS).
+ * (0: one per CPU of the process's affinity mask, or FASTDECODE_CPU_THREADS;
+ * at most FD_HOST_MAX_THREADS, larger counts are FD_ERR_INVALID).
  * Rows with lens <= 0 give out = 0, lse = -inf; a range error makes the row
  * NaN. Used to give part of each row's host-tier blocks to the host cores
  * while the GPU reads the rest over the link; the two partials are then
@@ -330,9 +331,14 @@ int fd_host_decode_partial(
  * (cpu_attn.cpp:36-40,523). */
 int fd_host_decode_threads(void);
 
-/* Sets that count for the process (n <= 0 restores the default). Replaces
- * the extension's set_num_threads (cpu_attn.cpp:521). */
+/* Sets that count for the process (n <= 0 restores the default; n above
+ * FD_HOST_MAX_THREADS is FD_ERR_INVALID). Replaces the extension's
+ * set_num_threads (cpu_attn.cpp:521). */
 int fd_host_set_threads(int32_t n);
+
+/* Upper bound on the host-core worker count (a FASTDECODE_CPU_THREADS above
+ * it is clamped). */
+#define FD_HOST_MAX_THREADS 1024
 
 /* Division of each row's host-tier blocks between the GPU and the host cores
  * for the hybrid split (host code; no counterpart in the reference, whose

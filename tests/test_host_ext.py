@@ -149,6 +149,9 @@ def test_thread_controls_and_isa():
         l1 = torch.empty(8, 9)
         ext.decode_attn(q, kc, vc, bt, lens, 0.1, o1, l1)
         assert torch.equal(o1, o3) and torch.equal(l1, l3)
+        with pytest.raises(RuntimeError, match="at most 1024"):
+            ext.set_num_threads(1025)
+        assert ext.get_num_threads() == 1  # a refused count changes nothing
     finally:
         ext.set_num_threads(0)
     assert ext.get_num_threads() == default

@@ -446,7 +446,7 @@ int default_threads() {
   const int set_n = g_threads.load(std::memory_order_relaxed);
   if (set_n > 0) return set_n;
   const char* e = getenv("FASTDECODE_CPU_THREADS");
-  if (e != nullptr && atoi(e) > 0) return atoi(e);
+  if (e != nullptr && atoi(e) > 0) return std::min(atoi(e), FD_HOST_MAX_THREADS);
   cpu_set_t set;
   if (sched_getaffinity(0, sizeof(set), &set) == 0) return std::max(1, CPU_COUNT(&set));
   return std::max(1u, std::thread::hardware_concurrency());
@@ -493,6 +493,9 @@ extern "C" int fd_share_host_blocks(const int32_t* host_bt, int64_t bt_stride, i
 }
 
 extern "C" int fd_host_set_threads(int32_t n) {
+  if (n > FD_HOST_MAX_THREADS)
+    return set_error(FD_ERR_INVALID, "fd_host_set_threads: %d threads (at most %d)", n,
+                     FD_HOST_MAX_THREADS);
   g_threads.store(n > 0 ? n : 0, std::memory_order_relaxed);
   return FD_OK;
 }
@@ -541,7 +544,7 @@ extern "C" int fd_host_decode_partial(
     int32_t num_threads) {
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
       head_size <= 0 || head_size > 1024 || block_size <= 0 || block_size > 1024 ||
-      bt_width < 0 || num_blocks < 0 || num_threads < 0)
+      bt_width < 0 || num_blocks < 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: bad sizes");
   if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: unsupported kv dtype %d", kv_dtype);
