@@ -284,7 +284,10 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     gp.out_dt = a.out_dtype;
     gp.lse = a.lse;
     gp.lse_sh = a.lse_sh;
-    hipLaunchKernelGGL(decode_generic_kernel, dim3((unsigned)a.n * a.H), dim3(kWave), 0, s, gp);
+    if ((int64_t)a.n * a.H > INT32_MAX)
+      return set_error(FD_ERR_UNSUPPORTED, "decode: too many (sequence, head) pairs");
+    hipLaunchKernelGGL(decode_generic_kernel, dim3((unsigned)((int64_t)a.n * a.H)), dim3(kWave),
+                       0, s, gp);
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? FD_OK : hip_error(e, "decode_generic_kernel launch");
   }
