@@ -447,3 +447,37 @@ def test_block_offsets_past_4gib(gpu):
     assert_lse_close(l, ref_lse, mask=nz)
     del phys
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("H,KVH,D", [(32, 2, 128), (32, 1, 128), (64, 4, 64), (16, 1, 256)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_head_groups_past_eight_match_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatch):
+    """More than 8 query heads per kv head (16, 32, multi-query): the tiled
+    kernels run passes of 8 heads over the same blocks. Host layout and
+    vLLM's layout, whole rows and forced 2-block splits, lengths 0, 1,
+    partial and whole blocks."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    n, BS, C = len(GQA_LENS), 16, 96
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=160,
+                                          seed=H + KVH + D)
+    lens[:] = torch.tensor(GQA_LENS, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    # the same blocks in vLLM's [B, BS, KVH, 2D] layout
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, torch.float32, gpu)
+        assert_out_close(out, ref_out, 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+        o_v = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        o_v, l_v = ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu),
+                                    lens.to(gpu), scale, out=o_v)
+        torch.cuda.synchronize()
+        assert_out_close(o_v, ref_out, 2e-3, mask=nz)
+        assert_lse_close(l_v, ref_lse, mask=nz)

@@ -285,3 +285,16 @@ def test_fused_long_rows(gpu, kernel, H, KVH, dtype, monkeypatch):
     nz = c["lens"] > 0
     check_vs_oracle(out, lse, ref, ref_lse, nz)
     assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
+@pytest.mark.parametrize("kernel", ["default", "valu"])
+def test_fused_head_groups_past_eight(gpu, kernel, monkeypatch):
+    """Fused two-tier launch with 16 query heads per kv head (passes of 8)."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    c = two_tier_case(9, 32, 2, 128, torch.bfloat16, seed=61, dev=gpu)
+    out, lse = run_fused(c, gpu)
+    ref, ref_lse = oracle_merged(c)
+    nz = c["lens"] > 0
+    check_vs_oracle(out, lse, ref, ref_lse, nz)
+    assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))

@@ -84,7 +84,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Task t;
-  if (!decode_task<TWO>(p, t)) return;
+  if (!decode_task<G, TWO>(p, t)) return;
   if (t.nb == 0 || t.range_bad) {
     if (t.split == 0 && wave == 0) write_empty<T, D, G>(p, t, lane);
     return;
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
   Vec8 qb[KS];
   {
     const uint16_t* qrow =
-        p.q + (int64_t)t.i * p.q_ss + (int64_t)(t.kh * G + hg) * p.q_sh + R * 8;
+        p.q + (int64_t)t.i * p.q_ss + (int64_t)(t.h0 + hg) * p.q_sh + R * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qb[ks] = ld16(qrow + 32 * ks);
   }

@@ -235,9 +235,12 @@ int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
                       int32_t bt_width, int32_t kv_dtype, bool aligned) {
   SplitPlan sp{};
+  sp.passes = 1;
   const int G = KVH > 0 ? H / KVH : 0;
+  // groups of more than 8 query heads per kv head (a multiple of 8: 16, 32,
+  // multi-query ...) run as passes of 8 heads, each re-reading the blocks
   sp.fast = aligned && BS == kTileTokens && (D == 64 || D == 128 || D == 256) &&
-            (G == 1 || G == 2 || G == 4 || G == 8) &&
+            (G == 1 || G == 2 || G == 4 || (G >= 8 && G % 8 == 0 && G <= kMaxHeadGroup)) &&
             (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
   if (!sp.fast) {
     sp.split_blocks = bt_width > 0 ? bt_width : 1;
@@ -245,9 +248,11 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     return sp;
   }
   sp.mfma = G >= 4 && !valu_forced();
+  sp.passes = G > 8 ? G / 8 : 1;
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
-  if (sb <= 0) sb = model_split_blocks(n, H, KVH, D, BS, bt_width);
+  // each pass streams the blocks once more: model it as that many kv heads
+  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, BS, bt_width);
   sp.split_blocks = sb;
   sp.max_splits = bt_width > 0 ? (bt_width + sb - 1) / sb : 1;
   const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=0: natural occupancy (tuning)
@@ -320,6 +325,8 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   tp.n = a.n;
   tp.H = a.H;
   tp.KVH = a.KVH;
+  tp.hpk = a.H / a.KVH;
+  tp.passes = sp.passes;
   tp.scale_log2 = a.scale * kLog2e;
   tp.out = a.out;
   tp.out_ss = a.out_ss;
@@ -335,9 +342,9 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     tp.part_o = reinterpret_cast<float*>(ws);
     tp.part_lse = reinterpret_cast<float*>(ws + parts * a.D * sizeof(float));
   }
-  const int64_t tasks = (int64_t)a.n * a.KVH * sp.max_splits;
+  const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
-  const int G = a.H / a.KVH;
+  const int G = a.H / a.KVH / sp.passes;  // the kernel's heads per task
   hipError_t e = sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
                          : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");

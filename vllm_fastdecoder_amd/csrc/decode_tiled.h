@@ -41,6 +41,7 @@ constexpr int kWavesPerTask = 4;        // wavefronts sharing one task
 constexpr int kMaxWaveBlocks = kWave;   // a wave's block ids of a task fit one VGPR
 constexpr int kMaxSplitBlocks = kWavesPerTask * kMaxWaveBlocks;
 constexpr int kMaxDevices = 64;         // per-device launch settings cached
+constexpr int kMaxHeadGroup = 512;      // largest H / KVH the tiled kernels take (in passes of 8)
 
 // One KV tier as the tiled kernels see it (16-bit elements).
 struct TierParams {
@@ -63,6 +64,8 @@ struct TiledParams {
   TierParams tier[2];    // tier[1] is read by two-tier launches only
   const int32_t* order;  // optional processing order of the sequences
   int32_t n, H, KVH;
+  int32_t hpk;     // query heads per kv head (H / KVH)
+  int32_t passes;  // head groups per kv head: hpk / the kernel's G (> 1 only for G = 8)
   float scale_log2;  // softmax scale * log2(e)
   void* out;
   int64_t out_ss, out_sh;
@@ -202,13 +205,15 @@ __device__ __forceinline__ void store8(void* out, int64_t off, bool f32, const f
 // blocks are tier 0's nba blocks followed by tier 1's.
 struct Task {
   int i, kh, split;
+  int h0;  // first query head of the task: kh * hpk + its head group * G
   int la, lb;  // tokens of the row in tier 0 / tier 1 (<= 0: none)
   int nba, nb;
   int b_begin, b_end, nsplit;
   bool range_bad;  // a length needs more blocks than its table has
 };
 
-// blockIdx.x -> task: kv head fastest, then sequence (in the caller's order
+// blockIdx.x -> task: kv head fastest, then head group (one unless a kv head
+// has more query heads than the kernel's G), then sequence (in the caller's order
 // when one is given, e.g. longest rows first so the last workgroups dispatched
 // are short ones), split slowest. Split-major order matters on this GPU:
 // workgroups are dealt round-robin to the XCDs and, inside an XCD, to its
@@ -217,11 +222,16 @@ struct Task {
 // engines and idle them; split-major keeps the empty ones together at the end.
 // False when the workgroup has nothing to do: an order entry outside [0, n),
 // or a split past the row's last block.
-template <bool TWO>
+template <int G, bool TWO>
 __device__ __forceinline__ bool decode_task(const TiledParams& p, Task& t) {
   const int task = blockIdx.x;
   t.kh = task % p.KVH;
-  const int rest = task / p.KVH;
+  int rest = task / p.KVH;
+  // a kv head with more than G query heads (G = 8, hpk a multiple of 8) is
+  // done in passes of G heads, each its own task over the same blocks
+  const int pass = rest % p.passes;
+  rest /= p.passes;
+  t.h0 = t.kh * p.hpk + pass * G;
   t.split = rest / p.n;
   int i = rest % p.n;
   if (p.order != nullptr) {
@@ -259,7 +269,7 @@ __device__ __forceinline__ void write_empty(const TiledParams& p, const Task& t,
   const float fill = t.range_bad ? qnan() : 0.f;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int h = t.kh * G + g;
+    const int h = t.h0 + g;
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = fill;
@@ -367,7 +377,7 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = qnan();
     }
-    const int h = t.kh * G + g;
+    const int h = t.h0 + g;
     if (lane < LPT) {
       if (write_final) {
         store8<T>(p.out, (int64_t)t.i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8,

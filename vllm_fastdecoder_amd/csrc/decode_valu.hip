@@ -36,7 +36,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   // indexing derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Task t;
-  if (!decode_task<TWO>(p, t)) return;
+  if (!decode_task<G, TWO>(p, t)) return;
   if (t.nb == 0 || t.range_bad) {
     if (t.split == 0 && wave == 0) write_empty<T, D, G>(p, t, lane);
     return;
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   Vec8 qf[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int h = t.kh * G + g;
+    const int h = t.h0 + g;
     qf[g] = ld16(p.q + (int64_t)i * p.q_ss + (int64_t)h * p.q_sh + chunk * 8);
   }
 
