@@ -35,8 +35,8 @@
  *   - Strides are in elements, not bytes. The innermost (head_size)
  *     dimension must be contiguous and 16-byte aligned for the fast kernels,
  *     which take block_size 16, head_size 64 / 128 / 256, fp16 / bf16 and
- *     num_heads / num_kv_heads in {1, 2, 4} or a multiple of 8 up to 512;
- *     other shapes and layouts take a slower generic kernel.
+ *     num_heads / num_kv_heads up to 512; other shapes and layouts take a
+ *     slower generic kernel.
  */
 #ifndef FDATTN_H_
 #define FDATTN_H_

@@ -450,12 +450,15 @@ def test_block_offsets_past_4gib(gpu):
 
 
 @pytest.mark.parametrize("kernel", ["mfma", "valu"])
-@pytest.mark.parametrize("H,KVH,D", [(32, 2, 128), (32, 1, 128), (64, 4, 64), (16, 1, 256)])
+@pytest.mark.parametrize("H,KVH,D", [(32, 2, 128), (32, 1, 128), (64, 4, 64), (16, 1, 256),
+                                     (24, 8, 128), (40, 8, 128), (12, 2, 64), (28, 4, 128),
+                                     (48, 4, 256)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_head_groups_past_eight_match_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatch):
-    """More than 8 query heads per kv head (16, 32, multi-query): the tiled
-    kernels run passes of 8 heads over the same blocks. Host layout and
-    vLLM's layout, whole rows and forced 2-block splits, lengths 0, 1,
+def test_any_head_group_matches_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatch):
+    """Query heads per kv head outside {1, 2, 4, 8}: 3 in a 4-slot kernel,
+    5-7 in an 8-slot one (spare slots write nothing), 12, 16, 32 and
+    multi-query as passes of up to 8 heads over the same blocks. Host layout
+    and vLLM's layout, whole rows and forced 2-block splits, lengths 0, 1,
     partial and whole blocks."""
     if kernel == "valu":
         monkeypatch.setenv("FD_DECODE_KERNEL", "valu")

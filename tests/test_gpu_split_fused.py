@@ -288,11 +288,13 @@ def test_fused_long_rows(gpu, kernel, H, KVH, dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("kernel", ["default", "valu"])
-def test_fused_head_groups_past_eight(gpu, kernel, monkeypatch):
-    """Fused two-tier launch with 16 query heads per kv head (passes of 8)."""
+@pytest.mark.parametrize("H,KVH", [(32, 2), (40, 8), (28, 4)])
+def test_fused_any_head_group(gpu, kernel, H, KVH, monkeypatch):
+    """Fused two-tier launch with 16 (passes of 8), 5 and 7 (8-slot kernel)
+    query heads per kv head."""
     if kernel == "valu":
         monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
-    c = two_tier_case(9, 32, 2, 128, torch.bfloat16, seed=61, dev=gpu)
+    c = two_tier_case(9, H, KVH, 128, torch.bfloat16, seed=61 + H, dev=gpu)
     out, lse = run_fused(c, gpu)
     ref, ref_lse = oracle_merged(c)
     nz = c["lens"] > 0

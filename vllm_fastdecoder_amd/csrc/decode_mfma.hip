@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
   Vec8 qb[KS];
   {
     const uint16_t* qrow =
-        p.q + (int64_t)t.i * p.q_ss + (int64_t)(t.h0 + hg) * p.q_sh + R * 8;
+        p.q + (int64_t)t.i * p.q_ss + (int64_t)task_head(t, hg) * p.q_sh + R * 8;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qb[ks] = ld16(qrow + 32 * ks);
   }

@@ -237,18 +237,20 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   SplitPlan sp{};
   sp.passes = 1;
   const int G = KVH > 0 ? H / KVH : 0;
-  // groups of more than 8 query heads per kv head (a multiple of 8: 16, 32,
-  // multi-query ...) run as passes of 8 heads, each re-reading the blocks
+  // The tiled kernels are built for 1, 2, 4 or 8 query heads per task: a
+  // group of 3 runs in a 4-head kernel, of 5-7 in an 8-head one (the spare
+  // head slots repeat a real head and write nothing), and more than 8 heads
+  // per kv head run as passes of up to 8, each re-reading the blocks.
+  sp.kernel_g = G <= 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
   sp.fast = aligned && BS == kTileTokens && (D == 64 || D == 128 || D == 256) &&
-            (G == 1 || G == 2 || G == 4 || (G >= 8 && G % 8 == 0 && G <= kMaxHeadGroup)) &&
-            (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
+            G >= 1 && G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
   if (!sp.fast) {
     sp.split_blocks = bt_width > 0 ? bt_width : 1;
     sp.max_splits = 1;
     return sp;
   }
   sp.mfma = G >= 4 && !valu_forced();
-  sp.passes = G > 8 ? G / 8 : 1;
+  sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   // each pass streams the blocks once more: model it as that many kv heads
@@ -344,7 +346,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   }
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
-  const int G = a.H / a.KVH / sp.passes;  // the kernel's heads per task
+  const int G = sp.kernel_g;  // the kernel's head slots per task
   hipError_t e = sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
                          : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");

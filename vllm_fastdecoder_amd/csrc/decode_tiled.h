@@ -65,7 +65,7 @@ struct TiledParams {
   const int32_t* order;  // optional processing order of the sequences
   int32_t n, H, KVH;
   int32_t hpk;     // query heads per kv head (H / KVH)
-  int32_t passes;  // head groups per kv head: hpk / the kernel's G (> 1 only for G = 8)
+  int32_t passes;  // head groups per kv head: ceil(hpk / the kernel's G)
   float scale_log2;  // softmax scale * log2(e)
   void* out;
   int64_t out_ss, out_sh;
@@ -205,7 +205,9 @@ __device__ __forceinline__ void store8(void* out, int64_t off, bool f32, const f
 // blocks are tier 0's nba blocks followed by tier 1's.
 struct Task {
   int i, kh, split;
-  int h0;  // first query head of the task: kh * hpk + its head group * G
+  int h0;      // first query head of the task: kh * hpk + its head group * G
+  int gcount;  // query heads of the task (<= G; the kernel's other head slots
+               // repeat the last one and write nothing)
   int la, lb;  // tokens of the row in tier 0 / tier 1 (<= 0: none)
   int nba, nb;
   int b_begin, b_end, nsplit;
@@ -227,11 +229,12 @@ __device__ __forceinline__ bool decode_task(const TiledParams& p, Task& t) {
   const int task = blockIdx.x;
   t.kh = task % p.KVH;
   int rest = task / p.KVH;
-  // a kv head with more than G query heads (G = 8, hpk a multiple of 8) is
-  // done in passes of G heads, each its own task over the same blocks
+  // a kv head with more than G query heads is done in passes of up to G
+  // heads, each its own task over the same blocks
   const int pass = rest % p.passes;
   rest /= p.passes;
   t.h0 = t.kh * p.hpk + pass * G;
+  t.gcount = min(G, p.hpk - pass * G);
   t.split = rest / p.n;
   int i = rest % p.n;
   if (p.order != nullptr) {
@@ -269,6 +272,7 @@ __device__ __forceinline__ void write_empty(const TiledParams& p, const Task& t,
   const float fill = t.range_bad ? qnan() : 0.f;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+    if (g >= t.gcount) break;
     const int h = t.h0 + g;
     float o[8];
 #pragma unroll
@@ -378,7 +382,7 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
       for (int e = 0; e < 8; ++e) o[e] = qnan();
     }
     const int h = t.h0 + g;
-    if (lane < LPT) {
+    if (g < t.gcount && lane < LPT) {
       if (write_final) {
         store8<T>(p.out, (int64_t)t.i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8,
                   p.out_f32, o);
@@ -390,6 +394,12 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
       }
     }
   }
+}
+
+// Query head of the task's head slot g: slots past the task's heads repeat
+// its last head (their results are never written).
+__device__ __forceinline__ int task_head(const Task& t, int g) {
+  return t.h0 + min(g, t.gcount - 1);
 }
 
 // The cache run of a wave's block k: K and V buffer resources over its

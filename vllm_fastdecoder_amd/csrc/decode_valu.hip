@@ -50,7 +50,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   Vec8 qf[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int h = t.h0 + g;
+    const int h = task_head(t, g);
     qf[g] = ld16(p.q + (int64_t)i * p.q_ss + (int64_t)h * p.q_sh + chunk * 8);
   }
 

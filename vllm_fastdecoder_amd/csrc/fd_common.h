@@ -186,8 +186,9 @@ struct SplitPlan {
   bool fast;             // the tiled kernel applies (else the generic one)
   bool mfma;             // grouped-query scores on the matrix cores (G >= 4)
   bool cap_occupancy;    // long tasks: at most two workgroups per CU
-  int32_t passes;        // head groups of the tiled kernel's G per kv head (G = H/KVH
-                         // above 8: passes of 8 heads over the same blocks), else 1
+  int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4 or 8
+  int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
+                         // kernel_g), each over the same blocks
 };
 
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
