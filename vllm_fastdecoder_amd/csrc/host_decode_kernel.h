@@ -263,24 +263,30 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
     if (bid < 0 || bid >= a.num_blocks) return false;
     const int ntok = std::min(BS, L - b * BS);
     const int64_t base = bid * a.sb + (int64_t)kh * a.sh;
-    if (b + kPrefetchBlocks < nb) {  // a later block's rows, while this one computes
+    int64_t nbase = -1;  // a later block's rows, prefetched a few at a time below
+    if (b + kPrefetchBlocks < nb) {
       const int64_t nid = row_bt[b + kPrefetchBlocks];
-      if (nid >= 0 && nid < a.num_blocks) {
-        const int64_t nbase = nid * a.sb + (int64_t)kh * a.sh;
-        for (int t = 0; t < BS; ++t)
-          for (int off = 0; off < D * elt; off += 64) {
-            _mm_prefetch(kbase + (nbase + (int64_t)t * a.st) * elt + off, _MM_HINT_T0);
-            _mm_prefetch(vbase + (nbase + (int64_t)t * a.st) * elt + off, _MM_HINT_T0);
-          }
-      }
+      if (nid >= 0 && nid < a.num_blocks) nbase = nid * a.sb + (int64_t)kh * a.sh;
     }
+    int pf = 0;  // next row of that block to prefetch
+    auto prefetch_rows = [&](int upto) {
+      if (nbase < 0) return;
+      for (; pf < upto && pf < BS; ++pf)
+        for (int off = 0; off < D * elt; off += 64) {
+          _mm_prefetch(kbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
+          _mm_prefetch(vbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
+        }
+    };
     // scores, TT tokens at a time where the accumulators fit
     int t0 = 0;
     if constexpr (TT >= 2) {
-      for (; t0 + TT <= ntok; t0 += TT)
+      for (; t0 + TT <= ntok; t0 += TT) {
+        prefetch_rows(pf + TT);
         score_tokens<DT, G, TT>(kbase + (base + (int64_t)t0 * a.st) * elt, a.st * elt, qf, qh,
                                 qs, D, DW, s + t0, BS);
+      }
     }
+    prefetch_rows(BS);
     for (int t = t0; t < ntok; ++t)
       score_token<DT, G, U>(kbase + (base + (int64_t)t * a.st) * elt, qf, qh, qs, D, DW, s + t,
                             BS);
