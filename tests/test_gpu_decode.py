@@ -484,3 +484,38 @@ def test_any_head_group_matches_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatc
         torch.cuda.synchronize()
         assert_out_close(o_v, ref_out, 2e-3, mask=nz)
         assert_lse_close(l_v, ref_lse, mask=nz)
+
+
+@pytest.mark.parametrize("D", [32, 80, 96, 112, 160, 192, 200])
+@pytest.mark.parametrize("H,KVH", [(8, 8), (16, 4), (40, 8)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_head_sizes_between_kernels_match_oracle(gpu, D, H, KVH, dtype, monkeypatch):
+    """Head sizes other than 64 / 128 / 256 (any multiple of 8 up to 256) run
+    in the next larger VALU kernel with the spare lanes idle. Host layout and
+    vLLM's layout, whole rows and forced 2-block splits (the combine kernel
+    and its workspace at the real head size), fp32 and 16-bit outputs."""
+    n, BS, C = len(GQA_LENS), 16, 96
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=160,
+                                          seed=D + H + KVH)
+    lens[:] = torch.tensor(GQA_LENS, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    tol = OUT_TOL_16BIT[dtype]
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, torch.float32, gpu)
+        assert_out_close(out, ref_out, 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+        out16, lse16 = run_host_layout(q, kc, vc, bt, lens, scale, dtype, gpu)
+        assert_out_close(out16, ref_out, tol, tol, mask=nz)
+        assert torch.equal(lse16, lse)
+        o_v = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        o_v, l_v = ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu),
+                                    lens.to(gpu), scale, out=o_v)
+        torch.cuda.synchronize()
+        assert_out_close(o_v, ref_out, 2e-3, mask=nz)
+        assert_lse_close(l_v, ref_lse, mask=nz)

@@ -300,3 +300,14 @@ def test_fused_any_head_group(gpu, kernel, H, KVH, monkeypatch):
     nz = c["lens"] > 0
     check_vs_oracle(out, lse, ref, ref_lse, nz)
     assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
+@pytest.mark.parametrize("D", [80, 96])
+def test_fused_head_sizes_between_kernels(gpu, D):
+    """Fused two-tier launch at head sizes run in the next larger kernel."""
+    c = two_tier_case(9, 16, 4, D, torch.float16, seed=D, dev=gpu)
+    out, lse = run_fused(c, gpu)
+    ref, ref_lse = oracle_merged(c)
+    nz = c["lens"] > 0
+    check_vs_oracle(out, lse, ref, ref_lse, nz)
+    assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))

@@ -242,14 +242,17 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   // head slots repeat a real head and write nothing), and more than 8 heads
   // per kv head run as passes of up to 8, each re-reading the blocks.
   sp.kernel_g = G <= 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
-  sp.fast = aligned && BS == kTileTokens && (D == 64 || D == 128 || D == 256) &&
-            G >= 1 && G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
+  // head sizes are built for 64, 128 and 256; any other multiple of 8 up to
+  // 256 runs in the next larger one on the VALU kernel (its spare lanes idle)
+  sp.kernel_d = D <= 64 ? 64 : D <= 128 ? 128 : 256;
+  sp.fast = aligned && BS == kTileTokens && D % 8 == 0 && D >= 8 && D <= 256 && G >= 1 &&
+            G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
   if (!sp.fast) {
     sp.split_blocks = bt_width > 0 ? bt_width : 1;
     sp.max_splits = 1;
     return sp;
   }
-  sp.mfma = G >= 4 && !valu_forced();
+  sp.mfma = G >= 4 && D == sp.kernel_d && !valu_forced();
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
@@ -327,6 +330,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   tp.n = a.n;
   tp.H = a.H;
   tp.KVH = a.KVH;
+  tp.D = a.D;
   tp.hpk = a.H / a.KVH;
   tp.passes = sp.passes;
   tp.scale_log2 = a.scale * kLog2e;
@@ -348,7 +352,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
   const int G = sp.kernel_g;  // the kernel's head slots per task
   hipError_t e = sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
-                         : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s);
+                         : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, sp.kernel_d, G, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");
   if (sp.max_splits > 1) {
     const int64_t threads = (int64_t)a.n * a.H * (a.D / 4);

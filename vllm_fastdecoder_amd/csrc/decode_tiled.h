@@ -64,6 +64,7 @@ struct TiledParams {
   TierParams tier[2];    // tier[1] is read by two-tier launches only
   const int32_t* order;  // optional processing order of the sequences
   int32_t n, H, KVH;
+  int32_t D;       // head size (<= the kernel's D; lanes past it only stand by)
   int32_t hpk;     // query heads per kv head (H / KVH)
   int32_t passes;  // head groups per kv head: ceil(hpk / the kernel's G)
   float scale_log2;  // softmax scale * log2(e)
@@ -268,7 +269,7 @@ __device__ __forceinline__ int block_tokens(const Task& t, int u) {
 template <typename T, int D, int G>
 __device__ __forceinline__ void write_empty(const TiledParams& p, const Task& t, int lane) {
   constexpr int LPT = D / 8;
-  if (lane >= LPT) return;
+  if (lane >= LPT || lane * 8 >= p.D) return;
   const float fill = t.range_bad ? qnan() : 0.f;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -382,14 +383,14 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
       for (int e = 0; e < 8; ++e) o[e] = qnan();
     }
     const int h = t.h0 + g;
-    if (g < t.gcount && lane < LPT) {
+    if (g < t.gcount && lane < LPT && chunk * 8 < p.D) {
       if (write_final) {
         store8<T>(p.out, (int64_t)t.i * p.out_ss + (int64_t)h * p.out_sh + chunk * 8,
                   p.out_f32, o);
         if (lane == 0) p.lse[(int64_t)h * p.lse_sh + t.i] = lse_nat;
       } else {
         const int64_t pidx = ((int64_t)t.i * p.H + h) * p.S + t.split;
-        store8<T>(p.part_o, pidx * D + chunk * 8, true, o);
+        store8<T>(p.part_o, pidx * p.D + chunk * 8, true, o);
         if (lane == 0) p.part_lse[pidx] = lse_nat;
       }
     }

@@ -45,24 +45,30 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
 
   const int row = lane / LPT;    // which token of each load this lane owns
   const int chunk = lane % LPT;  // which 8-element slice of the row
+  // A head size below the kernel's D (e.g. 96 in the 128 kernel): lanes of
+  // the slices past it hold a zero query, load their token's first slice
+  // (in bounds, already fetched by the row's first lane) and are never stored.
+  const bool lane_on = chunk * 8 < p.D;
+  const int lchunk = lane_on ? chunk : 0;
 
   // ---- query fragments (unscaled, native precision)
   Vec8 qf[G];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int h = task_head(t, g);
-    qf[g] = ld16(p.q + (int64_t)i * p.q_ss + (int64_t)h * p.q_sh + chunk * 8);
+    qf[g] = lane_on ? ld16(p.q + (int64_t)i * p.q_ss + (int64_t)h * p.q_sh + chunk * 8)
+                    : Vec8{{0u, 0u, 0u, 0u}};
   }
 
   // Byte offset of this lane's 16 bytes inside one (block, head) run, per
   // tier; load step j adds j*step (a scalar operand). The same for every
   // block, so the loop only moves the wave-uniform base held in a scalar
   // buffer resource.
-  const uint32_t off0 = (uint32_t)(((int64_t)row * p.tier[0].st + chunk * 8) * 2);
+  const uint32_t off0 = (uint32_t)(((int64_t)row * p.tier[0].st + lchunk * 8) * 2);
   const uint32_t step0 = (uint32_t)((int64_t)TPW * p.tier[0].st * 2);
   uint32_t off1 = 0, step1 = 0;
   if constexpr (TWO) {
-    off1 = (uint32_t)(((int64_t)row * p.tier[1].st + chunk * 8) * 2);
+    off1 = (uint32_t)(((int64_t)row * p.tier[1].st + lchunk * 8) * 2);
     step1 = (uint32_t)((int64_t)TPW * p.tier[1].st * 2);
   }
   // ADJ: lanes [2 LPT c, 2 LPT c + LPT) read K and the next LPT lanes V of
@@ -72,7 +78,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   if constexpr (ADJ) {
     const int half = (lane / LPT) & 1;
     const int c = lane / (2 * LPT);
-    off_kv = (uint32_t)(((int64_t)(2 * c) * p.tier[0].st + half * D + chunk * 8) * 2);
+    off_kv = (uint32_t)(((int64_t)(2 * c) * p.tier[0].st + half * D + lchunk * 8) * 2);
     st_bytes = (uint32_t)(p.tier[0].st * 2);
   }
 
