@@ -34,9 +34,10 @@
  *     (see fd_host_alloc / fd_host_device_pointer).
  *   - Strides are in elements, not bytes. The innermost (head_size)
  *     dimension must be contiguous and 16-byte aligned for the fast kernels,
- *     which take block_size 16, a head_size that is a multiple of 8 up to
- *     256, fp16 / bf16 and num_heads / num_kv_heads up to 512; other shapes
- *     and layouts take a slower generic kernel.
+ *     which take a block_size that is a multiple of 16 up to 1024, a
+ *     head_size that is a multiple of 8 up to 256, fp16 / bf16 and
+ *     num_heads / num_kv_heads up to 512; other shapes and layouts take a
+ *     slower generic kernel.
  */
 #ifndef FDATTN_H_
 #define FDATTN_H_

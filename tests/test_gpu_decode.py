@@ -519,3 +519,37 @@ def test_head_sizes_between_kernels_match_oracle(gpu, D, H, KVH, dtype, monkeypa
         torch.cuda.synchronize()
         assert_out_close(o_v, ref_out, 2e-3, mask=nz)
         assert_lse_close(l_v, ref_lse, mask=nz)
+
+
+@pytest.mark.parametrize("BS", [32, 64, 256])
+@pytest.mark.parametrize("kernel", ["default", "valu"])
+@pytest.mark.parametrize("H,KVH,D,dtype", [(8, 8, 128, torch.float16), (16, 4, 128, torch.bfloat16),
+                                           (12, 2, 96, torch.float16)])
+def test_larger_cache_blocks_match_oracle(gpu, BS, kernel, H, KVH, D, dtype, monkeypatch):
+    """Cache blocks of 16 * m tokens run as m 16-token tiles: host layout and
+    vLLM's layout, whole rows and forced 2-tile splits (a split boundary
+    inside a cache block), lengths 0, 1, partial and whole blocks."""
+    if kernel == "valu":
+        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    lens_list = [0, 1, BS - 1, BS, BS + 1, 3 * BS + 5, 7, 2 * BS]
+    n, C = len(lens_list), 40
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=4 * BS,
+                                          seed=BS + H + D)
+    lens[:] = torch.tensor(lens_list, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, torch.float32, gpu)
+        assert_out_close(out, ref_out, 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+        o_v = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        o_v, l_v = ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu),
+                                    lens.to(gpu), scale, out=o_v)
+        torch.cuda.synchronize()
+        assert_out_close(o_v, ref_out, 2e-3, mask=nz)
+        assert_lse_close(l_v, ref_lse, mask=nz)

@@ -32,14 +32,14 @@ TOL16 = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
 
 
 def two_tier_case(n, H, KVH, D, dtype, seed, dev, G=512, C=512, lo=128, hi=1024,
-                  gpu_first=True, special=True):
+                  gpu_first=True, special=True, BS=16):
     """Rows of lens ~ U[lo, hi]; row i's first k_i blocks (k_i ~ U[0, nb_i])
     come from the HBM tier (ids < G), the rest from the pinned host tier.
     gpu_first=False interleaves the tiers and then gives each tier's last
     block a random token count, so both tiers of a row end in a partial block
     (the fused entry allows it; only the per-tier oracle covers it). special:
-    row 0 all on the host, row 1 all in HBM, row 2 empty."""
-    BS = 16
+    row 0 all on the host, row 1 all in HBM, row 2 empty. BS: tokens per
+    cache block."""
     g = torch.Generator().manual_seed(seed)
     lens = torch.randint(lo, hi + 1, (n,), generator=g, dtype=torch.int32)
     if special:
@@ -311,3 +311,16 @@ def test_fused_head_sizes_between_kernels(gpu, D):
     nz = c["lens"] > 0
     check_vs_oracle(out, lse, ref, ref_lse, nz)
     assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
+@pytest.mark.parametrize("BS", [32, 64])
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 32, torch.float16), (32, 8, torch.bfloat16)])
+def test_fused_larger_cache_blocks(gpu, BS, H, KVH, dtype):
+    """Cache blocks of 32 and 64 tokens (2 and 4 tiles of 16 to the kernels),
+    tiers interleaved so both end in partial blocks."""
+    c = two_tier_case(9, H, KVH, 128, dtype, seed=BS + H, dev=gpu, BS=BS, G=256, C=256,
+                      gpu_first=False)
+    out, lse = run_fused(c, gpu)
+    ref, ref_lse = oracle_merged(c)
+    nz = c["lens"] > 0
+    check_vs_oracle(out, lse, ref, ref_lse, nz)

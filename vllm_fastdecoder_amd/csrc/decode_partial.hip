@@ -245,7 +245,9 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   // head sizes are built for 64, 128 and 256; any other multiple of 8 up to
   // 256 runs in the next larger one on the VALU kernel (its spare lanes idle)
   sp.kernel_d = D <= 64 ? 64 : D <= 128 ? 128 : 256;
-  sp.fast = aligned && BS == kTileTokens && D % 8 == 0 && D >= 8 && D <= 256 && G >= 1 &&
+  // cache blocks of 16 * m tokens are m 16-token tiles to the tiled kernels
+  sp.fast = aligned && BS % kTileTokens == 0 && BS <= kMaxBlockSize && D % 8 == 0 && D >= 8 &&
+            D <= 256 && G >= 1 &&
             G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
   if (!sp.fast) {
     sp.split_blocks = bt_width > 0 ? bt_width : 1;
@@ -254,12 +256,15 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   }
   sp.mfma = G >= 4 && D == sp.kernel_d && !valu_forced();
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
+  // tasks, splits and the model count 16-token tiles (BS / 16 per block)
+  const int64_t tiles = (int64_t)(bt_width > 0 ? bt_width : 0) * (BS / kTileTokens);
+  const int32_t wt = (int32_t)std::min<int64_t>(tiles, INT32_MAX);
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   // each pass streams the blocks once more: model it as that many kv heads
-  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, BS, bt_width);
+  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, kTileTokens, wt);
   sp.split_blocks = sb;
-  sp.max_splits = bt_width > 0 ? (bt_width + sb - 1) / sb : 1;
+  sp.max_splits = wt > 0 ? (wt + sb - 1) / sb : 1;
   const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=0: natural occupancy (tuning)
   sp.cap_occupancy = sb >= 32 && !(cap != nullptr && strcmp(cap, "0") == 0);
   return sp;
@@ -331,6 +336,8 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   tp.H = a.H;
   tp.KVH = a.KVH;
   tp.D = a.D;
+  tp.BS = a.BS;
+  tp.tpb = a.BS / kTileTokens;
   tp.hpk = a.H / a.KVH;
   tp.passes = sp.passes;
   tp.scale_log2 = a.scale * kLog2e;
@@ -358,8 +365,8 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     const int64_t threads = (int64_t)a.n * a.H * (a.D / 4);
     hipLaunchKernelGGL(combine_splits_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256),
                        0, s, tp.part_o, tp.part_lse, a.tier[0].lens,
-                       two ? a.tier[1].lens : nullptr, a.tier[0].bt_width,
-                       two ? a.tier[1].bt_width : 0, a.n, a.H, a.D, sp.max_splits,
+                       two ? a.tier[1].lens : nullptr, a.tier[0].bt_width * tp.tpb,
+                       two ? a.tier[1].bt_width * tp.tpb : 0, a.n, a.H, a.D, sp.max_splits,
                        sp.split_blocks, kTileTokens, a.out, a.out_ss, a.out_sh, a.out_dtype, a.lse,
                        a.lse_sh);
     e = hipGetLastError();

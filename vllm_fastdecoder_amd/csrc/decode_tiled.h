@@ -42,6 +42,7 @@ constexpr int kMaxWaveBlocks = kWave;   // a wave's block ids of a task fit one 
 constexpr int kMaxSplitBlocks = kWavesPerTask * kMaxWaveBlocks;
 constexpr int kMaxDevices = 64;         // per-device launch settings cached
 constexpr int kMaxHeadGroup = 512;      // largest H / KVH the tiled kernels take (in passes of 8)
+constexpr int kMaxBlockSize = 1024;     // largest cache block size they take (16-token tiles)
 
 // One KV tier as the tiled kernels see it (16-bit elements).
 struct TierParams {
@@ -65,6 +66,8 @@ struct TiledParams {
   const int32_t* order;  // optional processing order of the sequences
   int32_t n, H, KVH;
   int32_t D;       // head size (<= the kernel's D; lanes past it only stand by)
+  int32_t BS;      // cache block size: tpb 16-token tiles, each handled as a kernel block
+  int32_t tpb;     // tiles per cache block (BS / 16)
   int32_t hpk;     // query heads per kv head (H / KVH)
   int32_t passes;  // head groups per kv head: ceil(hpk / the kernel's G)
   float scale_log2;  // softmax scale * log2(e)
@@ -252,8 +255,7 @@ __device__ __forceinline__ bool decode_task(const TiledParams& p, Task& t) {
   if (t.split > 0 && t.b_begin >= t.nb) return false;
   t.b_end = min(t.nb, t.b_begin + p.split_blocks);
   t.nsplit = t.nb > 0 ? (t.nb + p.split_blocks - 1) / p.split_blocks : 1;
-  t.range_bad = t.la > p.tier[0].bt_width * kTileTokens ||
-                (TWO && t.lb > p.tier[1].bt_width * kTileTokens);
+  t.range_bad = t.la > p.tier[0].bt_width * p.BS || (TWO && t.lb > p.tier[1].bt_width * p.BS);
   return true;
 }
 
@@ -292,7 +294,8 @@ struct WaveBlocks {
   int first;   // the wave's first block index in the row
   int nw;      // blocks of this wave
   int k1;      // first of the wave's blocks in tier 1 (>= nw: none)
-  int my_bid;  // lane k: id of the wave's k-th block
+  int my_bid;  // lane k: id of the cache block holding the wave's k-th tile
+  int my_sub;  // lane k: that tile's index inside its cache block (0 when BS = 16)
   bool bad;
 };
 
@@ -304,22 +307,27 @@ __device__ __forceinline__ WaveBlocks wave_blocks(const TiledParams& p, const Ta
   w.nw = w.first < t.b_end ? (t.b_end - w.first + kWavesPerTask - 1) / kWavesPerTask : 0;
   w.k1 = TWO ? (t.nba > w.first ? (t.nba - w.first + kWavesPerTask - 1) / kWavesPerTask : 0)
              : w.nw;
-  int bid = 0;
+  int bid = 0, sub = 0;
   bool my_bad = false;
   if (lane < w.nw) {
+    // tile u of the row: tile u % tpb of the row's cache block u / tpb
     const int u = w.first + kWavesPerTask * lane;
     if (TWO && u >= t.nba) {
       const TierParams& tp = p.tier[1];
-      bid = tp.bt[(int64_t)t.i * tp.bt_stride + (u - t.nba)];
+      const int ut = u - t.nba;
+      bid = tp.bt[(int64_t)t.i * tp.bt_stride + ut / p.tpb];
+      sub = ut % p.tpb;
       my_bad = bid < 0 || (int64_t)bid >= tp.num_blocks;
     } else {
       const TierParams& tp = p.tier[0];
-      bid = tp.bt[(int64_t)t.i * tp.bt_stride + u];
+      bid = tp.bt[(int64_t)t.i * tp.bt_stride + u / p.tpb];
+      sub = u % p.tpb;
       my_bad = bid < 0 || (int64_t)bid >= tp.num_blocks;
     }
   }
   w.bad = __ballot(my_bad) != 0;
   w.my_bid = my_bad ? 0 : bid;
+  w.my_sub = my_bad ? 0 : sub;
   return w;
 }
 
@@ -417,9 +425,11 @@ __device__ __forceinline__ BlockSrc block_src(const TiledParams& p, const WaveBl
                                               int k) {
   const bool t1 = TWO && k >= wb.k1;
   const int bid = __builtin_amdgcn_readlane(wb.my_bid, k);
+  const int sub = __builtin_amdgcn_readlane(wb.my_sub, k);
   const TierParams& a = p.tier[0];
   const TierParams& b = p.tier[TWO ? 1 : 0];
-  const int64_t base = (int64_t)bid * (t1 ? b.sb : a.sb) + (int64_t)kh * (t1 ? b.sh : a.sh);
+  const int64_t base = (int64_t)bid * (t1 ? b.sb : a.sb) + (int64_t)kh * (t1 ? b.sh : a.sh) +
+                       (int64_t)sub * kTileTokens * (t1 ? b.st : a.st);
   const uint32_t rb = t1 ? b.run_bytes : a.run_bytes;
   BlockSrc s;
   s.k = make_rsrc((t1 ? b.k : a.k) + base, t1 ? b.k_run_bytes : a.k_run_bytes);
