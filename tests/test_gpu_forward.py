@@ -227,3 +227,19 @@ def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
         assert stats["split_steps"] > 100
     assert stats["max_err_vs_mono"] <= 3e-3
     assert stats["max_err_vs_f64"] <= 3e-3
+
+
+@pytest.mark.parametrize("planner,cpu_fraction", [("host", 0.0), ("device", 0.0), ("host", "auto")])
+def test_continuous_batching_simulation_32_token_blocks(gpu, planner, cpu_fraction):
+    """The same simulation with vLLM cache blocks of 32 tokens: planning, the
+    slot writes of both tiers, the fused launch (blocks as two 16-token
+    tiles) and the hybrid split, every step against the monolithic oracle."""
+    from tests.simulate import run_simulation
+
+    stats = run_simulation(steps=120, seed=7, device=gpu, BS=32, G=128, C=1024, planner=planner,
+                           cpu_fraction=cpu_fraction)
+    print({k: v for k, v in stats.items() if k != "failures"})
+    assert stats["failures"] == [], stats["failures"][:5]
+    assert stats["decode_rows"] > 300
+    assert stats["max_err_vs_mono"] <= 3e-3
+    assert stats["max_err_vs_f64"] <= 3e-3
