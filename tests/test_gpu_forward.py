@@ -243,3 +243,19 @@ def test_continuous_batching_simulation_32_token_blocks(gpu, planner, cpu_fracti
     assert stats["decode_rows"] > 300
     assert stats["max_err_vs_mono"] <= 3e-3
     assert stats["max_err_vs_f64"] <= 3e-3
+
+
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 8, torch.bfloat16), (40, 8, torch.float16)])
+@pytest.mark.parametrize("cpu_fraction", [0.0, "auto"])
+def test_continuous_batching_simulation_grouped_heads(gpu, H, KVH, dtype, cpu_fraction):
+    """The simulation at grouped-query head shapes (Llama-3's 4 and a 5-head
+    group), through the fused launch and the hybrid split."""
+    from tests.simulate import run_simulation
+
+    tol = 3e-3 if dtype == torch.float16 else 1.6e-2  # 16-bit output of the split path
+    stats = run_simulation(steps=120, seed=11, device=gpu, H=H, KVH=KVH, dtype=dtype,
+                           cpu_fraction=cpu_fraction, tol=tol)
+    print({k: v for k, v in stats.items() if k != "failures"})
+    assert stats["failures"] == [], stats["failures"][:5]
+    assert stats["decode_rows"] > 300
+    assert stats["max_err_vs_mono"] <= tol
