@@ -2,7 +2,7 @@
 
 Tests marked `gpu` need an MI355X; the rest run on any CPU. The HIP library
 is built in-tree by __graft_entry__.build(); tests only build it when no
-library exists yet (the GPU box uses the shipped one).
+library exists yet (a machine that received a built tree uses that one).
 """
 
 from __future__ import annotations
