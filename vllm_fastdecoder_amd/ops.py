@@ -16,6 +16,7 @@ caches must be pinned (see pinned.py); the kernels read them in place.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 
 import numpy as np
@@ -41,7 +42,14 @@ def _require(cond: bool, msg: str) -> None:
         raise RuntimeError(msg)
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream_for(t: torch.Tensor) -> int:
+    """Handle of the current stream on t's device (the raw query where torch
+    has it: it skips building a Stream object on every call)."""
+    if _RAW_STREAM is not None and t.device.index is not None:
+        return int(_RAW_STREAM(t.device.index))
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -76,10 +84,23 @@ class _Workspace:
 WORKSPACE = _Workspace()
 
 
+_WS_SIZES: dict = {}
+
+
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
-    size = ctypes.c_size_t()
-    _lib.check(_lib.load_lib().fd_paged_decode_workspace_size(n, H, KVH, D, BS, width, ctypes.byref(size)))
-    return int(size.value)
+    """Workspace a decode call of this shape needs (remembered per shape and
+    task-size override, which the library reads from FD_SPLIT_BLOCKS)."""
+    key = (n, H, KVH, D, BS, width, os.environ.get("FD_SPLIT_BLOCKS"))
+    size = _WS_SIZES.get(key)
+    if size is None:
+        c = ctypes.c_size_t()
+        _lib.check(_lib.load_lib().fd_paged_decode_workspace_size(n, H, KVH, D, BS, width,
+                                                                  ctypes.byref(c)))
+        size = int(c.value)
+        if len(_WS_SIZES) > 4096:
+            _WS_SIZES.clear()
+        _WS_SIZES[key] = size
+    return size
 
 
 def paged_decode_partial(
@@ -331,7 +352,6 @@ class _HostShareRunner:
 
     def submit(self, fn):
         import concurrent.futures
-        import os
 
         with self._lock:
             if self._ex is None or self._pid != os.getpid():
