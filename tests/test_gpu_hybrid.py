@@ -236,3 +236,30 @@ def test_failed_begin_leaves_the_device_usable(gpu):
     out, lse = run_hybrid(c, gpu, 0.5)
     ref_o, ref_l = oracle_merged(c)
     check(out, lse, ref_o, ref_l, c["lens"])
+
+
+def test_finish_on_another_stream_than_begin(gpu):
+    """begin on a side stream, finish (and the merge) on the default stream,
+    then a second split at once: each split is correct, and the second one's
+    reuse of the pinned staging waits for the first one's copies on both
+    streams."""
+    c = two_tier_case(6, 8, 2, 64, torch.float16, seed=47, dev=gpu)
+    q = c["q"].to(gpu)
+    n, H, D = q.shape
+    args = (q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"], c["hk"], c["hv"],
+            c["bt_c"], c["len_c"], c["scale"], 0.5)
+    ref_o, ref_l = oracle_merged(c)
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    outs = []
+    for _ in range(2):
+        out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+        lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+        with torch.cuda.stream(side):
+            h = ops.hybrid_split_begin(*args, out=out, lse=lse)
+        torch.cuda.current_stream(gpu).wait_stream(side)
+        h.finish()
+        outs.append((out, lse))
+    torch.cuda.synchronize()
+    for out, lse in outs:
+        check(out, lse, ref_o, ref_l, c["lens"])

@@ -289,7 +289,7 @@ class _HybridStaging:
 
     def __init__(self) -> None:
         self._bufs: dict[tuple[int, str], torch.Tensor] = {}
-        self._released: dict[int, torch.cuda.Event] = {}
+        self._released: dict[int, list[torch.cuda.Event]] = {}
         self._pending: set[int] = set()
         self._lock = threading.Lock()
 
@@ -300,16 +300,21 @@ class _HybridStaging:
                 raise RuntimeError("a hybrid split is already in flight on this device; "
                                    "finish() it before starting another")
             self._pending.add(idx)
-            ev = self._released.get(idx)
-        if ev is not None:
+            evs = self._released.get(idx, ())
+        for ev in evs:
             ev.synchronize()
         return idx
 
-    def release(self, idx: int, stream) -> None:
-        ev = torch.cuda.Event()
-        ev.record(stream)
+    def release(self, idx: int, streams) -> None:
+        """Frees device idx's buffers once the work enqueued so far on every
+        stream in `streams` (those whose copies read or write them) is done."""
+        evs = []
+        for s in dict.fromkeys(streams):  # distinct, in order
+            ev = torch.cuda.Event()
+            ev.record(s)
+            evs.append(ev)
         with self._lock:
-            self._released[idx] = ev
+            self._released[idx] = evs
             self._pending.discard(idx)
 
     def view(self, idx: int, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
@@ -370,9 +375,10 @@ class HybridSplit:
     waits for the latter and enqueues the merge."""
 
     def __init__(self, out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_fn=None, host_job=None,
-                 staging_idx=None):
+                 staging_idx=None, stream=None):
         self.out, self.lse = out, lse
-        self._staging_idx = staging_idx
+        # the staging set in use and the stream begin() enqueued its copies on
+        self._staging_idx, self._stream = staging_idx, stream
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
         self._o_cpu, self._l_cpu = o_cpu, l_cpu
         # the host cores' share, and its future on the background thread; both
@@ -384,7 +390,10 @@ class HybridSplit:
         self.gpu_finished_first: bool | None = None
 
     def _drop(self) -> None:
-        HYBRID_STAGING.release(self._staging_idx, torch.cuda.current_stream(self.out.device))
+        # begin's uploads and finish's copy of the host partial may sit on
+        # different streams if the caller switched streams in between
+        HYBRID_STAGING.release(self._staging_idx,
+                               (self._stream, torch.cuda.current_stream(self.out.device)))
         self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._job = self._fn = None
 
     def cancel(self) -> None:
@@ -411,6 +420,12 @@ class HybridSplit:
             # (saves the thread hand-off when finish follows begin at once)
             res = self._fn() if self._job.cancel() else self._job.result()
             self.cpu_seconds, self.gpu_finished_first = res
+            cur = torch.cuda.current_stream(dev)
+            if self._stream is not None and cur != self._stream:
+                # the GPU partial was allocated on begin's stream: keep the
+                # allocator from reusing it before this stream's merge reads it
+                self._o_gpu.record_stream(cur)
+                self._l_gpu.record_stream(cur)
             merge_attn_states(self.out, self._o_gpu, self._l_gpu,
                               self._o_cpu.to(dev, non_blocking=True),
                               self._l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
@@ -505,9 +520,10 @@ def hybrid_split_begin(
         # them (measured slower when the GPU side bounds the step)
         job = _HOST_SHARE.submit(host_share)
     except BaseException:
-        HYBRID_STAGING.release(idx, stream)
+        HYBRID_STAGING.release(idx, (stream,))
         raise
-    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_share, job, staging_idx=idx)
+    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_share, job, staging_idx=idx,
+                       stream=stream)
 
 
 def hybrid_split_decode(
