@@ -216,3 +216,17 @@ def test_host_entry_points_reject_bad_arguments():
     assert not kc.any()
     assert store() == _lib.FD_OK and kc[0, 0, 5].tolist() == [1.0] * 8
     assert lib.fd_host_set_threads(0) == _lib.FD_OK
+
+
+def test_missing_library_raises_instead_of_falling_back(monkeypatch, tmp_path):
+    """Without the built library every entry point raises: there is no
+    CPU or PyTorch path behind the kernels."""
+    from vllm_fastdecoder_amd import ops
+
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libfdattn.so")
+    with pytest.raises(RuntimeError, match="missing.*no fallback"):
+        _lib.load_lib()
+    monkeypatch.setattr(ops, "_WS_SIZES", {})
+    with pytest.raises(RuntimeError, match="missing"):
+        ops.workspace_bytes(3, 8, 8, 64, 16, 5)
