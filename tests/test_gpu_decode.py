@@ -553,3 +553,53 @@ def test_larger_cache_blocks_match_oracle(gpu, BS, kernel, H, KVH, D, dtype, mon
         torch.cuda.synchronize()
         assert_out_close(o_v, ref_out, 2e-3, mask=nz)
         assert_lse_close(l_v, ref_lse, mask=nz)
+
+
+def test_launches_on_two_streams_use_their_own_workspace(gpu):
+    """Two split launches (rows long enough that the combine kernel runs, so
+    both use the workspace) on two streams with nothing ordering them:
+    each gives the result it gives alone, bit for bit."""
+    D, BS, H, KVH = 128, 16, 32, 8
+
+    def case(lens, seed):
+        lens = torch.tensor(lens, dtype=torch.int32)
+        w = cases.Workload("two-streams", len(lens), H, KVH, D, BS, torch.bfloat16, 1,
+                           int(lens.max()), None, seed)
+        nb = (lens + BS - 1) // BS
+        pool, W = int(nb.sum()), int(nb.max())
+        perm = torch.randperm(pool, generator=torch.Generator().manual_seed(seed)).to(torch.int32)
+        bt = torch.zeros(w.n, W, dtype=torch.int32)
+        pos = 0
+        for i in range(w.n):
+            bt[i, : int(nb[i])] = perm[pos: pos + int(nb[i])]
+            pos += int(nb[i])
+        kc, vc, _ = cases.kv_pool(w, pool, "vllm", gpu)
+        assert ops.workspace_bytes(w.n, H, KVH, D, BS, W) > 0
+        return (cases.queries(w, gpu), kc, vc, bt.to(gpu), lens.to(gpu), w.scale)
+
+    a = case([16384 + 7, 5000, 0, 300], 13)
+    b = case([9000, 12000 + 3, 40], 14)
+
+    def run(c):
+        out = torch.empty(c[0].shape, dtype=torch.float32, device=gpu)
+        return ops.paged_decode(*c, out=out)
+
+    alone = [run(a), run(b)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)
+    results = []
+    for _ in range(3):
+        s1.wait_stream(torch.cuda.current_stream(gpu))
+        s2.wait_stream(torch.cuda.current_stream(gpu))
+        with torch.cuda.stream(s1):
+            ra = run(a)
+        with torch.cuda.stream(s2):
+            rb = run(b)
+        results.append((ra, rb))
+        torch.cuda.current_stream(gpu).wait_stream(s1)
+        torch.cuda.current_stream(gpu).wait_stream(s2)
+    torch.cuda.synchronize()
+    for ra, rb in results:
+        for got, ref in ((ra, alone[0]), (rb, alone[1])):
+            assert torch.equal(got[0], ref[0])
+            assert torch.equal(got[1], ref[1])

@@ -48,9 +48,16 @@ _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 def _stream_for(t: torch.Tensor) -> int:
     """Handle of the current stream on t's device (the raw query where torch
     has it: it skips building a Stream object on every call)."""
-    if _RAW_STREAM is not None and t.device.index is not None:
-        return int(_RAW_STREAM(t.device.index))
+    if t.device.index is not None:
+        return _current_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _current_stream(idx: int) -> int:
+    """Handle of the current stream on device idx."""
+    if _RAW_STREAM is not None:
+        return int(_RAW_STREAM(idx))
+    return torch.cuda.current_stream(idx).cuda_stream
 
 
 def _on_device(t: torch.Tensor, device: torch.device) -> torch.Tensor:
@@ -61,23 +68,30 @@ def _on_device(t: torch.Tensor, device: torch.device) -> torch.Tensor:
 
 
 class _Workspace:
-    """Grow-only device scratch per device for the split partials (the same
-    grow-only policy as the reference's PinnedStaging.get, state.py:115-124)."""
+    """Grow-only device scratch for the split partials (the same grow-only
+    policy as the reference's PinnedStaging.get, state.py:115-124), one
+    buffer per (device, stream): launches on one stream run in order and
+    share it, launches on different streams may overlap and get their own.
+    A buffer is allocated while its stream is current, so the caching
+    allocator reuses a replaced one only after that stream's earlier work."""
 
     def __init__(self) -> None:
-        self._bufs: dict[int, torch.Tensor] = {}
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+        """The workspace of the current stream on `device` (the stream the
+        caller's launch goes on), at least nbytes long."""
         if nbytes == 0:
             return None
         idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (idx, _current_stream(idx))
         with self._lock:
-            buf = self._bufs.get(idx)
+            buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
                 cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
                 buf = torch.empty(cap, dtype=torch.uint8, device=torch.device("cuda", idx))
-                self._bufs[idx] = buf
+                self._bufs[key] = buf
             return buf
 
 
