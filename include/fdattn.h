@@ -111,7 +111,9 @@ int fd_abi_version(void);
  *             strides (out_stride_seq, out_stride_head, 1)
  * lse         fp32, lse[h, i] at h*lse_stride_head + i
  * workspace   device scratch of >= fd_paged_decode_workspace_size(...) bytes
- *             (may be NULL when that size is 0)
+ *             (may be NULL when that size is 0). Launches on one stream may
+ *             share it; launches that may overlap (other streams) need one
+ *             each. Its contents need no clearing between calls.
  * ------------------------------------------------------------------------ */
 int fd_paged_decode_partial(
     const void* q, int64_t q_stride_seq, int64_t q_stride_head,
