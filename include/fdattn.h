@@ -295,6 +295,8 @@ int fd_check_slots(const int64_t* slots, int64_t m, int64_t capacity,
  * directly over the link with no staging copy.
  * ------------------------------------------------------------------------ */
 int fd_host_alloc(size_t bytes, void** host_ptr);
+/* Waits for the work enqueued on the current device, then frees the block;
+ * work on other devices that uses it is the caller's to finish first. */
 int fd_host_free(void* host_ptr);
 /* Device address of a pinned allocation made by fd_host_alloc. */
 int fd_host_device_pointer(void* host_ptr, void** device_ptr);

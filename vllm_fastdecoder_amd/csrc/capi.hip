@@ -360,6 +360,9 @@ int fd_host_alloc(size_t bytes, void** host_ptr) {
 
 int fd_host_free(void* host_ptr) {
   if (host_ptr == nullptr) return FD_OK;
+  // kernels still enqueued on this device may read or write the block over
+  // the link: let them finish first (freeing is rare: a tier's teardown)
+  (void)hipDeviceSynchronize();
   const hipError_t e = hipHostFree(host_ptr);
   return e == hipSuccess ? FD_OK : hip_error(e, "hipHostFree");
 }
