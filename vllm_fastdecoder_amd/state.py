@@ -87,8 +87,9 @@ def ensure_store(num_gpu_blocks: int | None, num_cpu_blocks: int, block_size: in
         STORE = None
         return None
     if (STORE is not None and STORE.num_gpu_blocks == num_gpu_blocks
-            and STORE.num_cpu_blocks == num_cpu_blocks
-            and all(n in STORE.k for n in layer_names)):
+            and STORE.num_cpu_blocks == num_cpu_blocks and STORE.block_size == block_size
+            and STORE.num_kv_heads == num_kv_heads and STORE.head_size == head_size
+            and STORE.dtype == dtype and all(n in STORE.k for n in layer_names)):
         return STORE
     store = HostKVStore(int(num_gpu_blocks), int(num_cpu_blocks), block_size, num_kv_heads,
                         head_size, dtype)
