@@ -118,3 +118,12 @@ def test_share_rejects_rows_past_their_table_and_handles_empty_tables():
     s = share_host_blocks(bt, torch.tensor([-5, 20], dtype=torch.int32), 16, 1.0)
     assert s.gpu_lens.tolist() == [0, 0] and s.cpu_lens.tolist() == [0, 20]
     assert s.cpu_bt[1].tolist() == [3, 4]
+
+
+def test_share_tuner_ignores_a_step_without_a_finishing_order():
+    from vllm_fastdecoder_amd.plan import ShareTuner
+
+    t = ShareTuner(start=0.5, step=0.01)
+    assert t.update(None) == 0.5
+    assert t.update(True) == pytest.approx(0.49)
+    assert t.update(False) == pytest.approx(0.5)

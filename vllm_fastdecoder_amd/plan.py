@@ -349,7 +349,9 @@ class ShareTuner:
         self.step = step
         self.lo, self.hi = lo, hi
 
-    def update(self, gpu_finished_first: bool) -> float:
+    def update(self, gpu_finished_first: bool | None) -> float:
+        if gpu_finished_first is None:  # no finishing order seen (a split with no rows)
+            return self.fraction
         delta = -self.step if gpu_finished_first else self.step
         self.fraction = min(self.hi, max(self.lo, self.fraction + delta))
         return self.fraction
