@@ -238,54 +238,15 @@ def threads_used():
     return int(_lib.load_lib().fd_host_decode_threads())
 
 
-def split_tiers(w, lens, bt, dev):
-    """The split-run layout: 60% of each row's blocks (the last ones) in
-    pinned host memory [C, KVH, BS, D], the rest in the HBM tier's vLLM
-    layout, each tier's tables compacted (seeded N(0,1) data)."""
-    import torch
-
-    from tests import cases
-    from vllm_fastdecoder_amd.pinned import pinned_empty
-
-    nb = (lens + w.BS - 1) // w.BS
-    n_host = torch.ceil(nb.double() * 0.6).to(torch.int32)
-    n_hbm = nb - n_host
-    W = bt.shape[1]
-    bt_g = torch.zeros(w.n, W, dtype=torch.int32)
-    bt_c = torch.zeros(w.n, W, dtype=torch.int32)
-    len_g = (n_hbm * w.BS).to(torch.int32)
-    len_c = (lens - len_g).to(torch.int32)
-    G = int(n_hbm.sum())
-    C = int(n_host.sum())
-    pg = pc = 0
-    for i in range(w.n):
-        a, b = int(n_hbm[i]), int(n_host[i])
-        bt_g[i, :a] = torch.arange(pg, pg + a, dtype=torch.int32)
-        bt_c[i, :b] = torch.arange(pc, pc + b, dtype=torch.int32)
-        pg += a
-        pc += b
-    kc_g, vc_g, kv = cases.kv_pool(w, max(G, 1), "vllm", dev)
-    hk = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
-    hv = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
-    # fill the host tier in slabs (N(0,1), seeded)
-    gen = torch.Generator(device=dev).manual_seed(4242)
-    slab = 2048
-    for t in (hk, hv):
-        for s in range(0, C, slab):
-            e = min(C, s + slab)
-            t[s:e].copy_(torch.randn(e - s, w.KVH, w.BS, w.D, generator=gen, device=dev).to(w.dtype).cpu())
-    return dict(bt_g=bt_g, bt_c=bt_c, len_g=len_g, len_c=len_c, G=G, C=C, kc_g=kc_g, vc_g=vc_g,
-                kv=kv, hk=hk, hv=hv)
-
-
 def hybrid_profile(w, lens, bt, q, frac, steps, warmup, stream):
     """Only hybrid split steps at a fixed host-core share (for a kernel trace
     of the GPU side): per-step time and the host cores' time."""
     import torch
 
+    from tests import cases
     from vllm_fastdecoder_amd import ops
 
-    t = split_tiers(w, lens, bt, q.device)
+    t = cases.split_tiers(w, lens, bt, q.device)
     out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=q.device)
     lse = torch.empty(w.H, w.n, dtype=torch.float32, device=q.device)
     bt_g_d = t["bt_g"].to(q.device)
@@ -309,10 +270,11 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     (ops.split_decode), the host cores alone, and the hybrid split."""
     import torch
 
+    from tests import cases
     from vllm_fastdecoder_amd import ops
 
     dev = q.device
-    t = split_tiers(w, lens, bt, dev)
+    t = cases.split_tiers(w, lens, bt, dev)
     bt_g, bt_c, len_g, len_c = t["bt_g"], t["bt_c"], t["len_g"], t["len_c"]
     G, C, kc_g, vc_g, kv, hk, hv = (t[k] for k in ("G", "C", "kc_g", "vc_g", "kv", "hk", "hv"))
     del t

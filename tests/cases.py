@@ -120,6 +120,47 @@ def kv_pool(w: Workload, pool: int, layout: str, device, seed_offset: int = 0):
     raise ValueError(layout)
 
 
+def split_tiers(w: Workload, lens: torch.Tensor, bt: torch.Tensor, dev):
+    """The split-run layout of a workload: the last ceil(0.6 * nb) blocks of
+    each row in pinned host memory [C, KVH, BS, D], the rest in the HBM
+    tier's vLLM layout [G, BS, KVH, 2D], each tier's table compacted in
+    sequence order (the planner's s_gpu_bt / s_cpu_bt) and its token counts
+    (HBM blocks are whole; the host tier holds the partial last block). Data
+    N(0,1), seeded. bt only gives the table width."""
+    from vllm_fastdecoder_amd.pinned import pinned_empty
+
+    nb = (lens + w.BS - 1) // w.BS
+    n_host = torch.ceil(nb.double() * 0.6).to(torch.int32)
+    n_hbm = nb - n_host
+    W = bt.shape[1]
+    bt_g = torch.zeros(w.n, W, dtype=torch.int32)
+    bt_c = torch.zeros(w.n, W, dtype=torch.int32)
+    len_g = (n_hbm * w.BS).to(torch.int32)
+    len_c = (lens - len_g).to(torch.int32)
+    G = int(n_hbm.sum())
+    C = int(n_host.sum())
+    pg = pc = 0
+    for i in range(w.n):
+        a, b = int(n_hbm[i]), int(n_host[i])
+        bt_g[i, :a] = torch.arange(pg, pg + a, dtype=torch.int32)
+        bt_c[i, :b] = torch.arange(pc, pc + b, dtype=torch.int32)
+        pg += a
+        pc += b
+    kc_g, vc_g, kv = kv_pool(w, max(G, 1), "vllm", dev)
+    hk = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
+    hv = pinned_empty((max(C, 1), w.KVH, w.BS, w.D), w.dtype)
+    # fill the host tier in slabs (N(0,1), seeded)
+    gen = torch.Generator(device=dev).manual_seed(4242)
+    slab = 2048
+    for t in (hk, hv):
+        for s in range(0, C, slab):
+            e = min(C, s + slab)
+            t[s:e].copy_(torch.randn(e - s, w.KVH, w.BS, w.D, generator=gen,
+                                     device=dev).to(w.dtype).cpu())
+    return dict(bt_g=bt_g, bt_c=bt_c, len_g=len_g, len_c=len_c, G=G, C=C, kc_g=kc_g, vc_g=vc_g,
+                kv=kv, hk=hk, hv=hv)
+
+
 def queries(w: Workload, device) -> torch.Tensor:
     g = torch.Generator().manual_seed(500 + w.seed)
     return torch.randn(w.n, w.H, w.D, generator=g).to(w.dtype).to(device)
