@@ -238,11 +238,13 @@ def test_failed_begin_leaves_the_device_usable(gpu):
     check(out, lse, ref_o, ref_l, c["lens"])
 
 
-def test_finish_on_another_stream_than_begin(gpu):
+@pytest.mark.parametrize("given", [True, False])
+def test_finish_on_another_stream_than_begin(gpu, given):
     """begin on a side stream, finish (and the merge) on the default stream,
     then a second split at once: each split is correct, and the second one's
     reuse of the pinned staging waits for the first one's copies on both
-    streams."""
+    streams. given=False: begin allocates out / lse itself (on the side
+    stream), and they stay valid for the finishing stream's work."""
     c = two_tier_case(6, 8, 2, 64, torch.float16, seed=47, dev=gpu)
     q = c["q"].to(gpu)
     n, H, D = q.shape
@@ -253,13 +255,29 @@ def test_finish_on_another_stream_than_begin(gpu):
     side.wait_stream(torch.cuda.current_stream(gpu))
     outs = []
     for _ in range(2):
-        out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
-        lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+        out = torch.empty(n, H, D, dtype=torch.float32, device=gpu) if given else None
+        lse = torch.empty(H, n, dtype=torch.float32, device=gpu) if given else None
         with torch.cuda.stream(side):
             h = ops.hybrid_split_begin(*args, out=out, lse=lse)
         torch.cuda.current_stream(gpu).wait_stream(side)
-        h.finish()
-        outs.append((out, lse))
+        out, lse = h.finish()
+        # fp32 copies on the finishing stream (begin's out is in q's dtype)
+        outs.append((out.float(), lse.clone()))
+        del h, out, lse
+        # new work on begin's stream while the merge may still be pending
+        with torch.cuda.stream(side):
+            junk = torch.full((n, H, D), 3.0, dtype=q.dtype, device=gpu)
+            junk += 1
     torch.cuda.synchronize()
+    nz = c["lens"] > 0
     for out, lse in outs:
-        check(out, lse, ref_o, ref_l, c["lens"])
+        if given:
+            check(out, lse, ref_o, ref_l, c["lens"])
+            continue
+        # out in q's dtype: the reference's 16-bit bar
+        tol = TOL16[q.dtype]
+        err = (out.double().cpu()[nz] - ref_o[nz]).abs() - tol * ref_o[nz].abs()
+        assert float(err.max()) <= tol
+        rel = (lse.double().cpu()[:, nz] - ref_l[:, nz]).abs() / ref_l[:, nz].abs().clamp(min=1)
+        assert float(rel.max()) <= 1e-4
+        assert torch.all(out.cpu()[~nz] == 0)

@@ -389,8 +389,10 @@ class HybridSplit:
     waits for the latter and enqueues the merge."""
 
     def __init__(self, out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_fn=None, host_job=None,
-                 staging_idx=None, stream=None):
+                 staging_idx=None, stream=None, owned=()):
         self.out, self.lse = out, lse
+        # those of out / lse that begin() allocated (on its stream)
+        self._owned = owned
         # the staging set in use and the stream begin() enqueued its copies on
         self._staging_idx, self._stream = staging_idx, stream
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
@@ -436,10 +438,11 @@ class HybridSplit:
             self.cpu_seconds, self.gpu_finished_first = res
             cur = torch.cuda.current_stream(dev)
             if self._stream is not None and cur != self._stream:
-                # the GPU partial was allocated on begin's stream: keep the
-                # allocator from reusing it before this stream's merge reads it
-                self._o_gpu.record_stream(cur)
-                self._l_gpu.record_stream(cur)
+                # the GPU partial (and out / lse when begin() allocated them)
+                # came from begin's stream: keep the allocator from reusing
+                # them before this stream's merge and later work are done
+                for t in (self._o_gpu, self._l_gpu, *self._owned):
+                    t.record_stream(cur)
             merge_attn_states(self.out, self._o_gpu, self._l_gpu,
                               self._o_cpu.to(dev, non_blocking=True),
                               self._l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
@@ -483,10 +486,13 @@ def hybrid_split_begin(
              "the host tier must be in host memory")
     n, H, D = q.shape
     dev = q.device
+    owned = []
     if out is None:
         out = torch.empty_like(q)
+        owned.append(out)
     if lse is None:
         lse = torch.empty(H, n, dtype=torch.float32, device=dev)
+        owned.append(lse)
     share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
     if n == 0:
         return HybridSplit(out, lse, None, None, None, None, None)
@@ -537,7 +543,7 @@ def hybrid_split_begin(
         HYBRID_STAGING.release(idx, (stream,))
         raise
     return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_share, job, staging_idx=idx,
-                       stream=stream)
+                       stream=stream, owned=tuple(owned))
 
 
 def hybrid_split_decode(
