@@ -222,13 +222,13 @@ def test_ensure_store_rebuilds_when_the_geometry_changes(gpu, monkeypatch):
 
     monkeypatch.setattr(state, "STORE", None)
     names = ["l0", "l1"]
-    s1 = state.ensure_store(8, 4, 16, 2, 64, torch.float16, names)
-    assert state.ensure_store(8, 4, 16, 2, 64, torch.float16, names) is s1
+    s1 = state.ensure_host_store(8, 4, 16, 2, 64, torch.float16, names)
+    assert state.ensure_host_store(8, 4, 16, 2, 64, torch.float16, names) is s1
     for args, shape, dtype in (((8, 4, 32, 2, 64, torch.float16), (4, 2, 32, 64), torch.float16),
                                ((8, 4, 16, 2, 64, torch.bfloat16), (4, 2, 16, 64), torch.bfloat16),
                                ((8, 4, 16, 2, 128, torch.float16), (4, 2, 16, 128), torch.float16)):
-        s = state.ensure_store(*args, names)
+        s = state.ensure_host_store(*args, names)
         assert s is not s1 and s.k["l1"].shape == shape and s.v["l0"].dtype == dtype
         assert int(s.k["l0"].abs().sum()) == 0
         s1 = s
-    assert state.ensure_store(8, 0, 16, 2, 64, torch.float16, names) is None
+    assert state.ensure_host_store(8, 0, 16, 2, 64, torch.float16, names) is None

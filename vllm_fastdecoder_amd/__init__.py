@@ -9,7 +9,8 @@ Python surface (mirrors the reference plugin's modules):
   ops      decode_attn / store_kv (cpu_ops extension ABI), paged_decode,
            merge_attn_states, reshape_and_cache (backend.OPS primitives)
   plan     build_host_plan / to_device (per-step execution plan)
-  state    HostKVStore over pinned host memory, ensure_store, staging
+  state    HostKVStore over pinned host memory, ensure_store
+  config   FASTDECODE_CPU_BLOCKS / FASTDECODE_CPU_KV_GB sizing, spec checks
   backend  HipOps seam and the _forward_split orchestration
 """
 

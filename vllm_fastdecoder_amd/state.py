@@ -1,46 +1,26 @@
 """Worker-side state: the host KV tier in pinned, GPU-mapped memory.
 
-Mirrors fastdecode/state.py:16-134 and fastdecode/config.py:20-59. The
-difference that matters: the reference allocates the host tier as pageable
-`torch.zeros` and stages q/k/v/o/lse through pinned buffers every layer;
-here the tier itself is pinned and mapped (pinned.pinned_zeros), so the
-decode and cache-write kernels reach it directly and no staging copy or
-host-side compute exists. `PinnedStaging` is kept for callers that still
-move data through host buffers.
+Mirrors fastdecode/state.py:16-90, with the tier sized from the same
+environment (config.py). The difference that matters: the reference
+allocates the host tier as pageable `torch.zeros` and stages q/k/v/o/lse
+through pinned buffers every layer (state.py:93-134); here the tier itself
+is pinned and mapped (pinned.pinned_zeros), so the decode and cache-write
+kernels reach it directly and no per-layer staging exists (the hybrid
+split's few small buffers live in ops).
 """
 
 from __future__ import annotations
 
 import logging
-import os
 import time
 from dataclasses import dataclass, field
 
 import torch
 
-from .pinned import pinned_empty, pinned_zeros
+from . import config
+from .pinned import pinned_zeros
 
 logger = logging.getLogger("fastdecode")
-
-ENV_CPU_BLOCKS = "FASTDECODE_CPU_BLOCKS"
-ENV_CPU_KV_GB = "FASTDECODE_CPU_KV_GB"
-
-
-def enabled() -> bool:
-    """A host tier is configured (config.py:25)."""
-    return bool(os.environ.get(ENV_CPU_BLOCKS) or os.environ.get(ENV_CPU_KV_GB))
-
-
-def resolve_num_cpu_blocks(per_block_bytes: int) -> int:
-    """Host-tier blocks from FASTDECODE_CPU_BLOCKS, else FASTDECODE_CPU_KV_GB
-    GiB divided by the bytes one block takes over all layers (config.py:41-59)."""
-    blocks = os.environ.get(ENV_CPU_BLOCKS)
-    if blocks:
-        return max(0, int(blocks))
-    gb = os.environ.get(ENV_CPU_KV_GB)
-    if gb:
-        return max(0, int(float(gb) * (1 << 30)) // per_block_bytes)
-    return 0
 
 
 @dataclass
@@ -74,12 +54,13 @@ CpuKVStore = HostKVStore
 STORE: HostKVStore | None = None
 
 
-def ensure_store(num_gpu_blocks: int | None, num_cpu_blocks: int, block_size: int,
-                 num_kv_heads: int, head_size: int, dtype: torch.dtype,
-                 layer_names: list[str]) -> HostKVStore | None:
-    """Create (idempotently) the worker's host tier (state.py:32-90, without
-    the vLLM config objects): nothing when G is unknown yet (profiling-time
-    builders) or when no host blocks are configured."""
+def ensure_host_store(num_gpu_blocks: int | None, num_cpu_blocks: int, block_size: int,
+                      num_kv_heads: int, head_size: int, dtype: torch.dtype,
+                      layer_names: list[str]) -> HostKVStore | None:
+    """Create (idempotently) the worker's host tier from explicit geometry:
+    nothing when G is unknown yet (profiling-time builders), none when no
+    host blocks are configured; rebuilt when the geometry or the layers
+    change. ensure_store below resolves the geometry as the reference does."""
     global STORE
     if num_gpu_blocks is None:
         return STORE
@@ -98,36 +79,36 @@ def ensure_store(num_gpu_blocks: int | None, num_cpu_blocks: int, block_size: in
         store.add_layer(name)
     elt = torch.empty((), dtype=dtype).element_size()
     gib = 2 * len(layer_names) * num_cpu_blocks * num_kv_heads * block_size * head_size * elt / (1 << 30)
-    logger.info("FastDecode: %d GPU blocks + %d host blocks (block_size=%d, %.2f GiB pinned "
-                "host KV for %d layers, allocated in %.1fs)", num_gpu_blocks, num_cpu_blocks,
-                block_size, gib, len(layer_names), time.time() - t0)
+    from . import _lib
+
+    lib = _lib.load_lib()  # loaded now so a missing library fails at start-up
+    logger.warning("FastDecode: %d GPU blocks + %d host blocks (block_size=%d, %.2f GiB pinned "
+                   "host KV for %d layers, allocated in %.1fs). Host-core kernel: %d-bit "
+                   "vectors, threads=%d", num_gpu_blocks, num_cpu_blocks, block_size, gib,
+                   len(layer_names), time.time() - t0, lib.fd_host_decode_isa(),
+                   lib.fd_host_decode_threads())
     STORE = store
     return store
 
 
-class PinnedStaging:
-    """Grow-only pinned host buffers (state.py:93-124)."""
-
-    def __init__(self) -> None:
-        self._bufs: dict[str, torch.Tensor] = {}
-
-    def get(self, name: str, shape: tuple[int, ...], dtype: torch.dtype) -> torch.Tensor:
-        numel = 1
-        for s in shape:
-            numel *= int(s)
-        buf = self._bufs.get(name)
-        if buf is None or buf.dtype != dtype or buf.numel() < numel:
-            cap = max(numel, 1, 2 * (buf.numel() if buf is not None else 0))
-            buf = pinned_empty((cap,), dtype)
-            self._bufs[name] = buf
-        return buf[:numel].view(shape)
-
-
-_STAGING: PinnedStaging | None = None
-
-
-def staging() -> PinnedStaging:
-    global _STAGING
-    if _STAGING is None:
-        _STAGING = PinnedStaging()
-    return _STAGING
+def ensure_store(vllm_config, spec, layer_names: list[str]) -> HostKVStore | None:
+    """The reference's entry point (state.py:32-90), called from the metadata
+    builder's constructor: no-op unless FASTDECODE_CPU_BLOCKS /
+    FASTDECODE_CPU_KV_GB is set; G from vllm_config.cache_config.num_gpu_blocks
+    (None while memory is being profiled: nothing happens); C from the
+    environment over the spec's page size and the layer count; the spec
+    validated (full attention, unquantised) before anything is allocated.
+    Returns the store (the reference returns None)."""
+    global STORE
+    if not config.enabled():
+        return None
+    num_gpu = vllm_config.cache_config.num_gpu_blocks
+    if num_gpu is None:
+        return STORE
+    num_cpu = config.resolve_num_cpu_blocks_from_spec(spec, len(layer_names))
+    if num_cpu <= 0:
+        STORE = None
+        return None
+    config.validate_spec(spec)
+    return ensure_host_store(int(num_gpu), num_cpu, spec.block_size, spec.num_kv_heads,
+                             spec.head_size, spec.dtype, layer_names)
