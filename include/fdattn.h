@@ -137,6 +137,34 @@ int fd_paged_decode_workspace_size(
     int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
     int32_t block_size, int32_t bt_width, size_t* bytes);
 
+/* Size of the device scratch behind fd_paged_decode_partial_noalloc. */
+#define FD_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* fd_paged_decode_partial without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc). No counterpart in the reference. Same arguments,
+ * kernels and results as fd_paged_decode_partial; the split workspace is a
+ * fixed array of FD_NOALLOC_SCRATCH_BYTES in each GPU's memory, held from
+ * the first call on that GPU until the process ends. Sizes whose workspace
+ * (fd_paged_decode_workspace_size) exceeds it are rejected with
+ * FD_ERR_WORKSPACE before anything is written. The call allocates nothing.
+ * Calls that may overlap on one GPU (other streams or threads) share the
+ * array and race: serialise them, or use fd_paged_decode_partial with a
+ * workspace each. The array needs no clearing between calls. */
+int fd_paged_decode_partial_noalloc(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens, const int32_t* row_order,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused split decode: both tiers of a row in one launch.
  *
