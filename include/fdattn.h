@@ -230,10 +230,13 @@ int fd_split_decode(
  *                          else slot_mapping[t];
  *   host_slot_mapping[t] = slot - num_gpu_blocks*block_size for a host slot,
  *                          else -1.
- * A host id past num_gpu_blocks + num_cpu_blocks, or a length needing more
- * than bt_width blocks, adds to *error_count (may be NULL) -- the
- * planner's RuntimeError, reported asynchronously; the row's lengths then
- * make the decode kernels write NaN for it. The outputs have width
+ * A host id past num_gpu_blocks + num_cpu_blocks, a host slot past
+ * (num_gpu_blocks + num_cpu_blocks) * block_size, or a length needing more
+ * than bt_width blocks, adds to *error_count (may be NULL) -- the planner's
+ * RuntimeError and store_kv's range check, reported asynchronously; such a
+ * row's lengths or ids make the decode kernels write NaN for it, and passing
+ * error_count as fd_reshape_and_cache's write_gate keeps the step's KV
+ * writes out of both tiers. The outputs have width
  * out_width >= bt_width and row stride out_stride. Feeding both tables to
  * fd_split_decode (HBM tier, host tier) decodes every row, P and S alike.
  * ------------------------------------------------------------------------ */
@@ -289,6 +292,11 @@ int fd_merge_attn_states(
  *   s >= num_blocks*block_size
  *                         not written; counted into *error_count when
  *                         error_count != NULL (a device int32).
+ * write_gate (may be NULL): a device int32 written by earlier work on
+ * `stream`, e.g. the error_count of fd_plan_tiers; when it is non-zero the
+ * launch writes nothing, so a step whose slots the planner found past the
+ * cache writes no KV at all (every slot checked before any write,
+ * cpu_attn.cpp:506-510). It must not be the same counter as error_count.
  * The copy is bit-exact. key/value strides are per token and per head
  * (the rows may be strided views of a fused qkv tensor).
  * cache strides: element offset of (block b, token t, head g) is
@@ -303,7 +311,7 @@ int fd_reshape_and_cache(
     int64_t cache_stride_head, int64_t num_blocks,
     const int64_t* slot_mapping, int32_t num_tokens,
     int32_t num_kv_heads, int32_t head_size, int32_t block_size,
-    int32_t dtype, int32_t* error_count,
+    int32_t dtype, int32_t* error_count, const int32_t* write_gate,
     void* stream);
 
 /* Host-side range check of host-resident slots before a write, the rule of
@@ -323,8 +331,9 @@ int fd_check_slots(const int64_t* slots, int64_t m, int64_t capacity,
  * directly over the link with no staging copy.
  * ------------------------------------------------------------------------ */
 int fd_host_alloc(size_t bytes, void** host_ptr);
-/* Waits for the work enqueued on the current device, then frees the block;
- * work on other devices that uses it is the caller's to finish first. */
+/* Waits for the work enqueued on every device, then frees the block. If a
+ * wait fails (a stream capture under way, say) the block is kept and the
+ * call returns FD_ERR_HIP: call it outside capture. */
 int fd_host_free(void* host_ptr);
 /* Device address of a pinned allocation made by fd_host_alloc. */
 int fd_host_device_pointer(void* host_ptr, void** device_ptr);

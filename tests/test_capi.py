@@ -113,9 +113,13 @@ def test_merge_and_cache_write_reject_bad_arguments():
     assert lib.fd_merge_attn_states(None, 64, 64, 0, None, 64, 64, 0, None, 1, None, 64, 64, 0,
                                     None, 1, None, 0, 0, 1, 64, None) == _lib.FD_OK  # empty
     assert lib.fd_reshape_and_cache(16, 64, 64, 16, 64, 64, 16, 16, 1, 1, 1, 4, None, 3, 1, 64,
-                                     16, 0, None, None) == _lib.FD_ERR_INVALID
+                                     16, 0, None, None, None) == _lib.FD_ERR_INVALID
     assert lib.fd_reshape_and_cache(16, 64, 64, 16, 64, 64, 16, 16, 1, 1, 1, 4, 16, 3, 0, 64,
-                                    16, 0, None, None) == _lib.FD_ERR_INVALID
+                                    16, 0, None, None, None) == _lib.FD_ERR_INVALID
+    # the write gate must be another counter than the one the launch adds to
+    assert lib.fd_reshape_and_cache(16, 64, 64, 16, 64, 64, 16, 16, 1, 1, 1, 4, 16, 3, 1, 64,
+                                    16, 0, 32, 32, None) == _lib.FD_ERR_INVALID
+    assert b"write_gate" in lib.fd_last_error()
     assert lib.fd_stream_copy(16, 16, 17, None) == _lib.FD_ERR_INVALID
     assert lib.fd_host_device_pointer(None, None) == _lib.FD_ERR_INVALID
 

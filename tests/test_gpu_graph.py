@@ -18,14 +18,22 @@ from vllm_fastdecoder_amd import ops
 pytestmark = pytest.mark.gpu
 
 
-def _replays(gpu, q, step, outs, n_replays=4):
+def _replays(gpu, q, step, outs, n_replays=4, ws_bytes=0):
     """Capture step() (which writes outs), then replay with fresh q values
-    and compare each replay with an eager step() on the same q."""
-    step()  # warm-up: workspace and launch settings exist before capture
+    and compare each replay with an eager step() on the same q. The capture
+    stream's split workspace (ws_bytes) is reserved before capture, so the
+    captured launches allocate nothing."""
+    step()  # warm-up: launch settings (and the eager stream's workspace) exist
     torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=gpu)
+    ops.reserve_workspace(side, ws_bytes)
+    before = dict(ops.WORKSPACE._bufs)
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=side):
         step()
+    # no workspace was allocated or replaced under capture
+    assert {k: v.data_ptr() for k, v in ops.WORKSPACE._bufs.items()} == \
+        {k: v.data_ptr() for k, v in before.items()}
     gen = torch.Generator(device=gpu).manual_seed(5)
     x = torch.randn(512, 512, device=gpu)
     for r in range(n_replays):
@@ -57,7 +65,9 @@ def test_paged_decode_in_a_graph(gpu, split, monkeypatch):
     def step():
         ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse)
 
-    _replays(gpu, q, step, [out, lse])
+    ws = ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1])
+    assert (ws > 0) == (split == "2")
+    _replays(gpu, q, step, [out, lse], ws_bytes=ws)
 
 
 def test_fused_split_in_a_graph(gpu):
@@ -73,4 +83,5 @@ def test_fused_split_in_a_graph(gpu):
         ops.split_decode(q, c["kv"][..., :D], c["kv"][..., D:], bt_g, len_g, c["hk"], c["hv"],
                          bt_c, len_c, c["scale"], out=out, lse=lse)
 
-    _replays(gpu, q, step, [out, lse])
+    _replays(gpu, q, step, [out, lse],
+             ws_bytes=ops.workspace_bytes(n, H, 32, D, 16, bt_g.shape[1] + bt_c.shape[1]))

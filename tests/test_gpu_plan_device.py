@@ -218,3 +218,55 @@ def test_forward_device_hybrid(gpu, dtype, monkeypatch):
     state.STORE = None
     for o in (out, out2):
         assert float((o.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("fault", ["host_slot", "host_block_id"])
+def test_device_planned_step_with_a_bad_host_id_writes_nothing_and_raises(gpu, monkeypatch,
+                                                                          fault):
+    """A step planned on the GPU with one host slot past the host tier, or one
+    host block id past it (the reference's planner raises for the latter,
+    plan.py:133-137, and store_kv checks every slot before any write,
+    cpu_attn.cpp:506-510): neither tier receives any of the step's KV, the
+    step's own check and the next step's builder raise the planner's
+    RuntimeError, and once raised the error does not come back."""
+    monkeypatch.setattr(backend, "OPS", _PrefillOps)
+    G, C, BS, H, KVH, D, dtype = 24, 40, 16, 8, 2, 128, torch.float16
+    sc = build_tiers(REQS16, G, C, H, KVH, D, BS, dtype, 5, gpu)
+    state.STORE = state.HostKVStore(G, C, BS, KVH, D, dtype, k={"l0": sc.host_k},
+                                    v={"l0": sc.host_v})
+    bt, slots = sc.bt.clone(), sc.slots.clone()
+    if fault == "host_slot":
+        slots[0] = (G + C) * BS + 3  # row 0's new token, past the host tier
+    else:
+        bt[5, 2] = G + C + 7  # row 5's third block (a host block), past the host tier
+    phys0, hk0, hv0 = sc.phys.clone(), sc.host_k.clone(), sc.host_v.clone()
+    impl = backend.SplitDecodeImpl(H, KVH, D, sc.scale)
+    layer = SimpleNamespace(layer_name="l0", _k_scale=None, _v_scale=None)
+    R = bt.shape[0]
+    out = torch.full_like(sc.query, float("nan"))
+    ds = backend.build_device_step(sc.qsl, sc.seq, bt.to(gpu), slots.to(gpu), R, state.STORE, gpu)
+    impl._forward_device(layer, sc.query, sc.key, sc.value, sc.kv_cache, ds, out)
+    torch.cuda.synchronize()
+    assert int(ds.errors.item()) == 1
+    assert torch.equal(sc.phys, phys0)
+    assert torch.equal(sc.host_k, hk0) and torch.equal(sc.host_v, hv0)
+    with pytest.raises(RuntimeError, match="beyond GPU\\+CPU capacity"):
+        ds.check_errors()
+    with pytest.raises(RuntimeError, match="beyond GPU\\+CPU capacity"):
+        backend.build_device_step(sc.qsl, sc.seq, bt.to(gpu), slots.to(gpu), R, state.STORE,
+                                  gpu)
+    # that second build was refused before planning: nothing is pending now,
+    # and a good step runs and checks clean
+    backend.raise_step_errors(wait=True)
+    ds = backend.build_device_step(sc.qsl, sc.seq, sc.bt.to(gpu), sc.slots.to(gpu), R,
+                                   state.STORE, gpu)
+    out = torch.full_like(sc.query, float("nan"))
+    impl._forward_device(layer, sc.query, sc.key, sc.value, sc.kv_cache, ds, out)
+    torch.cuda.synchronize()
+    ds.check_errors()
+    backend.raise_step_errors(wait=True)
+    state.STORE = None
+    assert float((out.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
+    phys = sc.phys.cpu()
+    assert torch.equal(phys[..., :D], sc.ref_k[:G]) and torch.equal(phys[..., D:], sc.ref_v[:G])
+    assert torch.equal(sc.host_k.transpose(1, 2), sc.ref_k[G:])

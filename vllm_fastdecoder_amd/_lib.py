@@ -18,7 +18,7 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 5
+ABI_VERSION = 6
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FD_NOALLOC_SCRATCH_BYTES of include/fdattn.h
 
 
@@ -131,7 +131,7 @@ SIGNATURES: dict[str, tuple] = {
             c_int64,                               # num_blocks
             c_void_p, c_int32,                     # slot_mapping, num_tokens
             c_int32, c_int32, c_int32,             # KVH, D, block_size
-            c_int32, c_void_p,                     # dtype, error_count
+            c_int32, c_void_p, c_void_p,           # dtype, error_count, write_gate
             c_void_p,                              # stream
         ],
     ),

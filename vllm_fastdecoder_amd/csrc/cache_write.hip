@@ -10,7 +10,11 @@
 //     [C, kv_heads, block_size, D] in pinned host memory written zero-copy.
 // The copy is bit-exact: bytes move unchanged, 16 at a time when every row
 // start is 16-byte aligned. A slot past the cache is never written; it is
-// counted into an optional device error counter instead.
+// counted into an optional device error counter instead. An optional write
+// gate (a device counter written by earlier work on the stream, e.g. the
+// tier planner's error count) stops the whole launch when it is non-zero,
+// so a step whose slots were found bad writes nothing (cpu_attn.cpp:506-510
+// checks every slot before any write).
 #include "fd_common.h"
 
 namespace fd {
@@ -26,6 +30,7 @@ __global__ __launch_bounds__(256) void cache_write_kernel(CacheWriteArgs a) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)a.T * a.KVH * pieces;
   if (tid >= total) return;
+  if (a.gate != nullptr && *a.gate != 0) return;
   const int c = (int)(tid % pieces);
   const int64_t rowid = tid / pieces;
   const int g = (int)(rowid % a.KVH);

@@ -151,7 +151,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 5; }
+int fd_abi_version(void) { return 6; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -302,7 +302,8 @@ int fd_reshape_and_cache(const void* key, int64_t key_stride_tok, int64_t key_st
                          int64_t cache_stride_head, int64_t num_blocks,
                          const int64_t* slot_mapping, int32_t num_tokens,
                          int32_t num_kv_heads, int32_t head_size, int32_t block_size,
-                         int32_t dtype, int32_t* error_count, void* stream) {
+                         int32_t dtype, int32_t* error_count, const int32_t* write_gate,
+                         void* stream) {
   if (num_tokens < 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
       num_blocks < 0)
     return set_error(FD_ERR_INVALID, "reshape_and_cache: bad sizes");
@@ -330,6 +331,9 @@ int fd_reshape_and_cache(const void* key, int64_t key_stride_tok, int64_t key_st
   a.BS = block_size;
   a.elt = dtype_size(dtype);
   a.err = error_count;
+  a.gate = write_gate;
+  if (write_gate != nullptr && write_gate == error_count)
+    return set_error(FD_ERR_INVALID, "reshape_and_cache: write_gate and error_count must differ");
   return launch_cache_write(a, static_cast<hipStream_t>(stream));
 }
 
@@ -360,10 +364,26 @@ int fd_host_alloc(size_t bytes, void** host_ptr) {
 
 int fd_host_free(void* host_ptr) {
   if (host_ptr == nullptr) return FD_OK;
-  // kernels still enqueued on this device may read or write the block over
-  // the link: let them finish first (freeing is rare: a tier's teardown)
-  (void)hipDeviceSynchronize();
-  const hipError_t e = hipHostFree(host_ptr);
+  // Kernels still enqueued on any device may read or write the block over
+  // the link: let them finish first (freeing is rare: a tier's teardown).
+  // If a wait fails (e.g. a stream capture is under way), the block is not
+  // freed: a leak, never a free under running kernels.
+  int count = 0, cur = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) return hip_error(e, "host_free: hipGetDeviceCount");
+  e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_error(e, "host_free: hipGetDevice");
+  for (int d = 0; d < count; ++d) {
+    e = hipSetDevice(d);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      (void)hipSetDevice(cur);
+      return hip_error(e, "host_free: waiting for the device's work (block kept)");
+    }
+  }
+  e = hipSetDevice(cur);
+  if (e != hipSuccess) return hip_error(e, "host_free: hipSetDevice");
+  e = hipHostFree(host_ptr);
   return e == hipSuccess ? FD_OK : hip_error(e, "hipHostFree");
 }
 

@@ -231,6 +231,7 @@ struct CacheWriteArgs {
   int32_t T, KVH, D, BS;
   int32_t elt;  // element size in bytes
   int32_t* err;
+  const int32_t* gate;  // nothing is written when *gate != 0 (may be NULL)
 };
 int launch_cache_write(const CacheWriteArgs& a, hipStream_t s);
 

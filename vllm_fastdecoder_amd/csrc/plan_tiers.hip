@@ -15,7 +15,9 @@
 // For every token t the slot mapping is split too (plan.py:150-152): a host
 // slot (>= G*BS) becomes -1 in gpu_slots and slot - G*BS in host_slots; any
 // other slot (negative padding included) keeps its value in gpu_slots and is
-// -1 in host_slots.
+// -1 in host_slots. A host slot past the host tier (>= (G+C)*BS) is counted
+// into *error_count too: the host-tier store_kv's range check
+// (cpu_attn.cpp:506-510), made before any write of the step.
 #include "fd_common.h"
 
 namespace fd {
@@ -73,14 +75,17 @@ __global__ __launch_bounds__(kWave) void plan_rows_kernel(PlanTiersArgs a) {
 
 __global__ __launch_bounds__(256) void plan_slots_kernel(const int64_t* __restrict__ slots,
                                                          int32_t n, int64_t hbm_slots,
+                                                         int64_t host_cap,
                                                          int64_t* __restrict__ gpu_slots,
-                                                         int64_t* __restrict__ host_slots) {
+                                                         int64_t* __restrict__ host_slots,
+                                                         int32_t* __restrict__ error_count) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= n) return;
   const int64_t s = slots[t];
   const bool on_host = s >= hbm_slots;
   gpu_slots[t] = on_host ? -1 : s;
   host_slots[t] = on_host ? s - hbm_slots : -1;
+  if (on_host && s - hbm_slots >= host_cap && error_count != nullptr) atomicAdd(error_count, 1);
 }
 
 }  // namespace
@@ -93,8 +98,8 @@ int launch_plan_tiers(const PlanTiersArgs& a, hipStream_t s) {
   }
   if (a.n_tokens > 0) {
     hipLaunchKernelGGL(plan_slots_kernel, dim3((unsigned)((a.n_tokens + 255) / 256)), dim3(256),
-                       0, s, a.slots, a.n_tokens, (int64_t)a.G * a.BS, a.gpu_slots,
-                       a.host_slots);
+                       0, s, a.slots, a.n_tokens, (int64_t)a.G * a.BS, a.C * a.BS,
+                       a.gpu_slots, a.host_slots, a.error_count);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_error(e, "plan_slots_kernel launch");
   }

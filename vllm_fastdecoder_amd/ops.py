@@ -73,29 +73,48 @@ class _Workspace:
     buffer per (device, stream): launches on one stream run in order and
     share it, launches on different streams may overlap and get their own.
     A buffer is allocated while its stream is current, so the caching
-    allocator reuses a replaced one only after that stream's earlier work."""
+    allocator reuses a replaced one only after that stream's earlier work.
+    At most `max_streams` buffers are kept; the least recently used one is
+    dropped beyond that (its memory returns to its stream's pool, which only
+    that stream's later allocations reuse)."""
 
-    def __init__(self) -> None:
+    def __init__(self, max_streams: int = 16) -> None:
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
         self._lock = threading.Lock()
+        self.max_streams = max_streams
 
-    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
-        """The workspace of the current stream on `device` (the stream the
-        caller's launch goes on), at least nbytes long."""
+    def get(self, device: torch.device, nbytes: int, stream: int | None = None
+            ) -> torch.Tensor | None:
+        """The workspace of `stream` (a raw handle; default: the current
+        stream on `device`, the one the caller's launch goes on), at least
+        nbytes long."""
         if nbytes == 0:
             return None
         idx = device.index if device.index is not None else torch.cuda.current_device()
-        key = (idx, _current_stream(idx))
+        key = (idx, _current_stream(idx) if stream is None else int(stream))
         with self._lock:
-            buf = self._bufs.get(key)
+            buf = self._bufs.pop(key, None)  # re-inserted below: most recent last
             if buf is None or buf.numel() < nbytes:
                 cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
                 buf = torch.empty(cap, dtype=torch.uint8, device=torch.device("cuda", idx))
-                self._bufs[key] = buf
+            self._bufs[key] = buf
+            while len(self._bufs) > self.max_streams:
+                del self._bufs[next(iter(self._bufs))]
             return buf
 
 
 WORKSPACE = _Workspace()
+
+
+def reserve_workspace(stream: torch.cuda.Stream, nbytes: int) -> None:
+    """Allocates the split workspace of `stream` now, at least nbytes long
+    (workspace_bytes of the largest shape to come). For HIP graph capture:
+    torch.cuda.graph captures on its own stream, so a workspace reserved for
+    that stream before capture keeps the captured launches from allocating
+    (otherwise the first captured launch of a shape that splits rows
+    allocates it from the graph's memory pool)."""
+    with torch.cuda.stream(stream):
+        WORKSPACE.get(stream.device, nbytes)
 
 
 _WS_SIZES: dict = {}
@@ -597,8 +616,8 @@ def plan_tiers(block_table: torch.Tensor, seq_lens: torch.Tensor, slot_mapping: 
 
     block_table int32 [R, W] on the GPU; seq_lens int32 [R] (a host tensor is
     uploaded, never read back); slot_mapping int64 [T] on the GPU;
-    error_count optional int32 [1] GPU counter of host ids past the host tier
-    and of lengths past the table. Returns (gpu_bt [R, W], cpu_bt [R, W],
+    error_count optional int32 [1] GPU counter of host ids past the host tier,
+    host slots past it and lengths past the table. Returns (gpu_bt [R, W], cpu_bt [R, W],
     gpu_lens [R], cpu_lens [R], gpu_slots [T], host_slots [T])."""
     _require(block_table.is_cuda and block_table.dtype == torch.int32 and block_table.dim() == 2,
              "block_table must be int32 [R, W] on the GPU")
@@ -779,8 +798,15 @@ def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
     )
 
 
+def _device_counter(t, what):
+    if t is None:
+        return None
+    _require(t.is_cuda and t.dtype == torch.int32, f"{what}: int32 GPU tensor")
+    return t.data_ptr()
+
+
 def _cache_write(key, value, k_cache, v_cache, strides_btg, num_blocks, block_size,
-                 slot_mapping, error_count) -> None:
+                 slot_mapping, error_count, write_gate=None) -> None:
     _require(key.dim() == 3 and value.shape == key.shape, "key/value must be [T, KVH, D]")
     T, KVH, D = key.shape
     _require(key.stride(2) == 1 and value.stride(2) == 1, "key/value must be contiguous in D")
@@ -792,10 +818,10 @@ def _cache_write(key, value, k_cache, v_cache, strides_btg, num_blocks, block_si
         return
     _require(key.is_cuda and value.is_cuda, "key/value must be on the GPU")
     slots = _on_device(slot_mapping, key.device).contiguous()
-    err_ptr = None
-    if error_count is not None:
-        _require(error_count.is_cuda and error_count.dtype == torch.int32, "error_count: int32 GPU")
-        err_ptr = error_count.data_ptr()
+    err_ptr = _device_counter(error_count, "error_count")
+    gate_ptr = _device_counter(write_gate, "write_gate")
+    _require(err_ptr is None or err_ptr != gate_ptr,
+             "error_count and write_gate must be different counters")
     _lib.check(
         _lib.load_lib().fd_reshape_and_cache(
             key.data_ptr(), key.stride(0), key.stride(1),
@@ -805,7 +831,7 @@ def _cache_write(key, value, k_cache, v_cache, strides_btg, num_blocks, block_si
             num_blocks,
             slots.data_ptr(), T,
             KVH, D, block_size,
-            _dtype_code(key, "key"), err_ptr,
+            _dtype_code(key, "key"), err_ptr, gate_ptr,
             _stream_for(key),
         )
     )
@@ -813,11 +839,15 @@ def _cache_write(key, value, k_cache, v_cache, strides_btg, num_blocks, block_si
 
 def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
                       kv_cache_dtype: str = "auto", k_scale=None, v_scale=None,
-                      error_count: torch.Tensor | None = None) -> None:
+                      error_count: torch.Tensor | None = None,
+                      write_gate: torch.Tensor | None = None) -> None:
     """vLLM reshape_and_cache_flash signature (fastdecode/backend.py:270-273):
     key_cache/value_cache [B, BS, KVH, D] views; slots < 0 are skipped.
     Only the unquantised cache ("auto"/fp16/bf16) is supported, as in the
-    reference backend (fastdecode/backend.py:68,211-212)."""
+    reference backend (fastdecode/backend.py:68,211-212).
+    error_count: int32 [1] GPU counter of slots past the cache (never written).
+    write_gate: int32 [1] GPU counter written by earlier work on the stream
+    (e.g. plan_tiers' error count); nothing is written when it is non-zero."""
     _require(kv_cache_dtype in ("auto", "float16", "bfloat16", "fp16", "bf16"),
              f"quantized KV cache ({kv_cache_dtype}) is not supported")
     _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape
@@ -829,7 +859,7 @@ def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping,
     _require(key.shape[0] >= T and value.shape[0] >= T, "fewer key/value rows than slots")
     _cache_write(key[:T], value[:T], key_cache, value_cache,
                  (key_cache.stride(0), key_cache.stride(1), key_cache.stride(2)),
-                 B, BS, slot_mapping, error_count)
+                 B, BS, slot_mapping, error_count, write_gate)
 
 
 def store_kv(k, v, slots, k_cache, v_cache) -> None:

@@ -24,12 +24,43 @@ from . import _lib
 _REG_LOCK = threading.Lock()
 _STARTS: list[int] = []          # sorted host start addresses
 _RANGES: dict[int, tuple[int, int]] = {}  # host start -> (nbytes, device start)
+# blocks whose last view died while a stream capture was under way: freeing
+# waits for the device, which a capture forbids, so they are freed by the
+# next allocation or free_deferred() outside capture
+_DEFERRED: list[int] = []
+
+
+def _capturing() -> bool:
+    try:
+        return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+    except RuntimeError:
+        return False
+
+
+def free_deferred() -> None:
+    """Frees the blocks released during a stream capture (no-op inside one)."""
+    if _capturing():
+        return
+    with _REG_LOCK:
+        todo = list(_DEFERRED)
+        _DEFERRED.clear()
+    for host in todo:
+        _free(host)
+
+
+def _free(host: int) -> None:
+    lib = _lib.load_lib()
+    if lib.fd_host_free(ctypes.c_void_p(host)) != _lib.FD_OK and \
+            b"block kept" in (lib.fd_last_error() or b""):
+        with _REG_LOCK:  # a wait failed and the block was kept: retry later
+            _DEFERRED.append(host)
 
 
 class _Allocation:
     """Owns one fd_host_alloc block; freed when the last tensor view dies."""
 
     def __init__(self, nbytes: int):
+        free_deferred()
         lib = _lib.load_lib()
         host = ctypes.c_void_p()
         _lib.check(lib.fd_host_alloc(nbytes, ctypes.byref(host)))
@@ -51,7 +82,10 @@ class _Allocation:
             if self.host in _RANGES:
                 del _RANGES[self.host]
                 _STARTS.remove(self.host)
-        _lib.load_lib().fd_host_free(ctypes.c_void_p(self.host))
+            if _capturing():
+                _DEFERRED.append(self.host)
+                return
+        _free(self.host)
 
 
 def pinned_empty(shape, dtype: torch.dtype, zero: bool = False) -> torch.Tensor:
