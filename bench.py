@@ -50,6 +50,11 @@ def parse_args():
     ap.add_argument("--layout", default="vllm", choices=["vllm", "host"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-split-run", action="store_true")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="skip the small-batch and Llama-3-8B decode legs of the default run")
+    ap.add_argument("--copies", type=int, default=None,
+                    help="pool copies rotated through by the measured workload (default: 5 for "
+                         "the small-batch workload, else 1)")
     ap.add_argument("--cpu-iters", type=int, default=20)
     ap.add_argument("--hybrid-profile", type=float, default=None, metavar="SHARE",
                     help="only run hybrid split steps of the workload's split layout at this "
@@ -389,6 +394,110 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     }
 
 
+def traffic_record(name: str, layout: str):
+    """HBM bytes per launch from the committed counter runs of this workload,
+    used only while they describe this exact kernel source."""
+    prof = ROOT / "profiles" / f"traffic_{name}_{layout}.json"
+    if not prof.exists():
+        return None
+    try:
+        rec = json.loads(prof.read_text())
+    except (ValueError, OSError):
+        return None
+    return rec.get("hbm_bytes_per_launch") if rec.get("source_sha256_16") == kernel_source_sha() \
+        else None
+
+
+def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False):
+    """Times one paged partial decode over every row's blocks of workload w,
+    all in HBM, rows scheduled longest first. copies > 1: that many copies of
+    the pool, launch k reading copy k % copies, so that a pool smaller than
+    the 256 MB Infinity Cache is not served from it on repeats (each copy of
+    the small-batch pool is 268 MB). graph: the timed launches are captured
+    in one HIP graph and replayed, as a serving engine issues its decode
+    step, so that Python's per-call overhead does not pad launches of a few
+    microseconds. Returns (ms per launch, algorithmic bytes, K+V bytes,
+    lens, timing note)."""
+    import torch
+
+    from tests import cases
+    from vllm_fastdecoder_amd import ops
+
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    pools = [cases.kv_pool(w, pool, layout, dev, seed_offset=c) for c in range(copies)]
+    q = cases.queries(w, dev)
+    bt_d, lens_d = bt.to(dev), lens.to(dev)
+    order_d = ops.longest_first(lens).to(dev)
+    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch(k):
+        kc, vc, _ = pools[k % copies]
+        if layout == "vllm":
+            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse,
+                             row_order=order_d)
+        else:
+            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse, row_order=order_d)
+
+    nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    if not graph:
+        counter = iter(range(1 << 62))
+        ms = time_gpu(lambda: launch(next(counter)), steps, warmup, stream)
+        note = f"HIP events around {steps} launches after {warmup} warm-ups"
+        return ms, nbytes, kvb, lens, note
+    for k in range(warmup):
+        launch(k)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=dev)
+    ops.reserve_workspace(side, ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1]))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for k in range(steps):
+            launch(k)
+    replays = 10
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        g.replay()
+    end.record(stream)
+    end.synchronize()
+    ms = start.elapsed_time(end) / (replays * steps)
+    note = (f"one HIP graph of {steps} launches over {copies} pool copies, HIP events around "
+            f"{replays} replays after {warmup} eager warm-ups")
+    del g, pools
+    return ms, nbytes, kvb, lens, note
+
+
+def leg_summary(w, layout, ms, nbytes, kvb, note, copies=1):
+    gbps = nbytes / (ms / 1e3) / 1e9
+    return {
+        "workload": (f"{w.name} decode attention, one layer: n={w.n}, {w.H}/{w.KVH} heads, "
+                     f"D={w.D}, BS={w.BS}, {str(w.dtype).replace('torch.', '')}, "
+                     f"L~U[{w.lo},{w.hi}], all blocks in HBM ({layout} layout)"
+                     + (f", {copies} pool copies rotated" if copies > 1 else "")),
+        "value": round(gbps, 1),
+        "unit": "GB/s",
+        "us_per_launch": round(ms * 1e3, 2),
+        "tokens_per_s": round(w.n / (ms / 1e3 * LAYERS), 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbps, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic_record(w.name, layout),
+            "algorithmic_bytes_per_launch": nbytes,
+            "kernel_ms": round(ms, 5),
+        },
+        "kv_bytes_per_launch": kvb,
+        "timing": note,
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -411,43 +520,26 @@ def main() -> int:
         print(json.dumps(hybrid_profile(w, lens, bt, cases.queries(w, dev), args.hybrid_profile,
                                         args.steps, args.warmup, torch.cuda.current_stream(dev))))
         return 0
-    if args.layout == "vllm":
-        kc, vc, _keep = cases.kv_pool(w, pool, "vllm", dev)
-    else:
-        kc, vc, _keep = cases.kv_pool(w, pool, "host", dev)
-    q = cases.queries(w, dev)
-    bt_d, lens_d = bt.to(dev), lens.to(dev)
-    # the planner's host-side scheduling order (rows longest first)
-    order_d = ops.longest_first(lens).to(dev)
-    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
-    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream(dev)
-
-    if args.layout == "vllm":
-        def step():
-            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse,
-                             row_order=order_d)
-    else:
-        def step():
-            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse, row_order=order_d)
-
-    elt = 2
-    nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, elt, elt)
-    ms = time_gpu(step, args.steps, args.warmup, stream)
+    # Legs run first, in this order: the small-batch shape (pool copies
+    # rotated past the Infinity Cache, launches replayed from a HIP graph) and
+    # the Llama-3-8B grouped-query shape, each with its own roofline; then the
+    # headline shape.
+    legs = {}
+    if args.workload == "vicuna7b" and not args.no_legs:
+        for name, copies, graph in (("correctness", 5, True), ("llama3_8b", 1, False)):
+            lw = cases.WORKLOADS[name]
+            ms_l, nb_l, kv_l, _, note = decode_leg(lw, "vllm", args.steps, args.warmup, dev,
+                                                  copies=copies, graph=graph)
+            key = "small_batch_leg" if name == "correctness" else "llama3_8b_leg"
+            legs[key] = leg_summary(lw, "vllm", ms_l, nb_l, kv_l, note, copies=copies)
+            torch.cuda.empty_cache()
+    copies = args.copies if args.copies is not None else (5 if w.name == "correctness" else 1)
+    ms, nbytes, kvb, _, timing = decode_leg(w, args.layout, args.steps, args.warmup, dev,
+                                            copies=copies, graph=w.name == "correctness")
     gbps = nbytes / (ms / 1e3) / 1e9
-
-    # HBM bytes per launch from the committed counter runs, used only while
-    # they describe this exact kernel source
-    traffic = None
-    prof = ROOT / "profiles" / f"traffic_{w.name}_{args.layout}.json"
-    if prof.exists():
-        sha = kernel_source_sha()
-        try:
-            rec = json.loads(prof.read_text())
-            if rec.get("source_sha256_16") == sha:
-                traffic = rec.get("hbm_bytes_per_launch")
-        except (ValueError, OSError):
-            traffic = None
+    traffic = traffic_record(w.name, args.layout)
+    q = cases.queries(w, dev)
+    stream = torch.cuda.current_stream(dev)
 
     result = {
         "metric": METRIC,
@@ -466,7 +558,8 @@ def main() -> int:
             "workload": (f"{w.name} decode attention, one layer: n={w.n}, {w.H}/{w.KVH} heads, "
                          f"D={w.D}, BS={w.BS}, L~U[{w.lo},{w.hi}], all blocks in HBM "
                          f"({'vLLM [B,BS,KVH,2D]' if args.layout == 'vllm' else 'host [C,KVH,BS,D]'} layout), "
-                         "rows scheduled longest-first"),
+                         "rows scheduled longest-first"
+                         + (f", {copies} pool copies rotated" if copies > 1 else "")),
             "global_batch": w.n,
             "seq_len": w.hi,
             "parallelism": "single GPU",
@@ -484,8 +577,9 @@ def main() -> int:
         "tokens_per_s": round(w.n / (ms / 1e3 * LAYERS), 1),
         "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "kv_bytes_per_step": kvb,
+        "timing": timing,
+        **legs,
     }
-    del _keep, kc, vc
     torch.cuda.empty_cache()
     if not args.no_split_run and w.name in ("vicuna7b", "llama3_8b"):
         result["split_run"] = split_run(w, lens, bt, q, args.steps, args.warmup, stream)

@@ -220,6 +220,7 @@ def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
                            cpu_fraction=cpu_fraction)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
+    assert stats["rows_vs_f64"] >= stats["decode_rows"] // 20  # every row of every 10th step
     assert stats["decode_rows"] > 1000
     if planner == "device":
         assert stats["device_planned_steps"] > 250
@@ -240,6 +241,7 @@ def test_continuous_batching_simulation_32_token_blocks(gpu, planner, cpu_fracti
                            cpu_fraction=cpu_fraction)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
+    assert stats["rows_vs_f64"] >= stats["decode_rows"] // 20  # every row of every 10th step
     assert stats["decode_rows"] > 300
     assert stats["max_err_vs_mono"] <= 3e-3
     assert stats["max_err_vs_f64"] <= 3e-3
@@ -257,5 +259,6 @@ def test_continuous_batching_simulation_grouped_heads(gpu, H, KVH, dtype, cpu_fr
                            cpu_fraction=cpu_fraction, tol=tol)
     print({k: v for k, v in stats.items() if k != "failures"})
     assert stats["failures"] == [], stats["failures"][:5]
+    assert stats["rows_vs_f64"] >= stats["decode_rows"] // 20  # every row of every 10th step
     assert stats["decode_rows"] > 300
     assert stats["max_err_vs_mono"] <= tol
