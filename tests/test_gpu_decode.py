@@ -221,16 +221,18 @@ def test_full_size_workloads_match_oracle(gpu, name):
 GQA_LENS = [0, 1, 15, 16, 17, 93, 160, 47]
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("kernel", ["default", "mfma", "valu"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("D", [64, 128, 256])
 @pytest.mark.parametrize("G", [4, 8])
 def test_gqa_kernels_match_oracle(gpu, kernel, dtype, D, G, monkeypatch):
-    """Grouped-query rows (G = 4, 8) on the matrix-core kernel (default) and on
+    """Grouped-query rows (G = 4, 8) on each kernel: the default (scores on
+    the matrix cores at G = 4 and at D = 256; scores and P.V there at G = 8,
+    D <= 128), the scores-only matrix-core kernel (FD_DECODE_KERNEL=mfma) and
     the VALU kernel (FD_DECODE_KERNEL=valu): lengths 0, 1, a partial block,
     exactly one block, one token past it; whole rows and forced 2-block splits."""
-    if kernel == "valu":
-        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    if kernel != "default":
+        monkeypatch.setenv("FD_DECODE_KERNEL", kernel)
     KVH = 2
     H = G * KVH
     n, BS, C = len(GQA_LENS), 16, 96
@@ -449,19 +451,20 @@ def test_block_offsets_past_4gib(gpu):
     torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("kernel", ["mfma", "valu"])
+@pytest.mark.parametrize("kernel", ["default", "mfma", "valu"])
 @pytest.mark.parametrize("H,KVH,D", [(32, 2, 128), (32, 1, 128), (64, 4, 64), (16, 1, 256),
                                      (24, 8, 128), (40, 8, 128), (12, 2, 64), (28, 4, 128),
-                                     (48, 4, 256)])
+                                     (48, 4, 256), (54, 2, 64), (96, 2, 128)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_any_head_group_matches_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatch):
     """Query heads per kv head outside {1, 2, 4, 8}: 3 in a 4-slot kernel,
     5-7 in an 8-slot one (spare slots write nothing), 12, 16, 32 and
-    multi-query as passes of up to 8 heads over the same blocks. Host layout
-    and vLLM's layout, whole rows and forced 2-block splits, lengths 0, 1,
-    partial and whole blocks."""
-    if kernel == "valu":
-        monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    multi-query as passes of up to 8 heads over the same blocks (16 on the
+    kernel with P.V on the matrix cores, the default for 5+ heads at D <= 128:
+    27 = 16 + 11, 48 = 3 x 16). Host layout and vLLM's layout, whole rows and
+    forced 2-block splits, lengths 0, 1, partial and whole blocks."""
+    if kernel != "default":
+        monkeypatch.setenv("FD_DECODE_KERNEL", kernel)
     n, BS, C = len(GQA_LENS), 16, 96
     q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=160,
                                           seed=H + KVH + D)
@@ -524,7 +527,8 @@ def test_head_sizes_between_kernels_match_oracle(gpu, D, H, KVH, dtype, monkeypa
 @pytest.mark.parametrize("BS", [32, 64, 256])
 @pytest.mark.parametrize("kernel", ["default", "valu"])
 @pytest.mark.parametrize("H,KVH,D,dtype", [(8, 8, 128, torch.float16), (16, 4, 128, torch.bfloat16),
-                                           (12, 2, 96, torch.float16)])
+                                           (12, 2, 96, torch.float16), (32, 4, 128, torch.float16),
+                                           (24, 2, 64, torch.bfloat16)])
 def test_larger_cache_blocks_match_oracle(gpu, BS, kernel, H, KVH, D, dtype, monkeypatch):
     """Cache blocks of 16 * m tokens run as m 16-token tiles: host layout and
     vLLM's layout, whole rows and forced 2-tile splits (a split boundary

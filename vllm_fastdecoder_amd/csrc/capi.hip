@@ -108,12 +108,15 @@ int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_s
   }
   SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
                              (int32_t)width, kv_dtype, aligned);
-  // Over the link the matrix-core kernel's K tiles (16 token rows of 16 bytes
+  // Over the link the matrix-core kernels' K tiles (16 token rows of 16 bytes
   // per lane group) read slower than the VALU kernel's whole rows (measured
   // on a GQA-4 host tier: 47.9 against 55.9 GB/s; in HBM the two are within
   // 3 %), so launches that read pinned host memory take the VALU kernel.
-  for (int t = 0; sp.mfma && t < a.ntiers; ++t)
-    if (in_host_memory(a.tier[t].k)) sp.mfma = false;
+  bool host = false;
+  for (int t = 0; (sp.mfma || sp.mm) && t < a.ntiers; ++t) host = host || in_host_memory(a.tier[t].k);
+  if (host)
+    sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, (int32_t)width, kv_dtype,
+                     aligned, false);
   const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return set_error(FD_ERR_WORKSPACE,
@@ -160,10 +163,16 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
       bt_width < 0)
     return set_error(FD_ERR_INVALID, "workspace_size: bad sizes");
-  // The aligned fast path is the only one that needs workspace; size for it.
-  const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
-                                   bt_width, FD_F16, true);
-  *bytes = decode_workspace_bytes(sp, n, num_heads, head_size);
+  // The aligned fast path is the only one that needs workspace; size for it,
+  // with or without the matrix-core kernels (a tier in pinned host memory
+  // takes the VALU kernel, whose head passes may split rows differently).
+  const SplitPlan a = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
+                                  FD_F16, true, true);
+  const SplitPlan b = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
+                                  FD_F16, true, false);
+  const size_t wa = decode_workspace_bytes(a, n, num_heads, head_size);
+  const size_t wb = decode_workspace_bytes(b, n, num_heads, head_size);
+  *bytes = wa > wb ? wa : wb;
   return FD_OK;
 }
 

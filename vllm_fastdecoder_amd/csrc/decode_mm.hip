@@ -1,0 +1,369 @@
+// Grouped-query decode kernel with both products on the matrix cores, for
+// groups of 5 to 16 query heads per kv head (larger groups in passes of 16).
+//
+// Per 16-token block of one kv head and up to 16 of its query heads (the
+// "columns"; spare columns repeat the task's last head and are never
+// written):
+//   scores  S[16 tokens x 16 columns] = K . Q^T: one v_mfma_f32_16x16x32 per
+//           32 dims, as in decode_mfma.hip; lane l ends with the scores of
+//           tokens 4R..4R+3 (R = l/16) for column l%16;
+//   softmax per column in the exp2 domain: the block max over the 16 tokens
+//           (an in-lane max of 4, then across the four 16-lane rows), a
+//           running max raised only when a block max passes it by more than
+//           kLazyRescale (so p <= 2^8), p = exp2(s - m);
+//   P.V     O[16 columns x D] += P . V: one v_mfma_f32_16x16x16 per 16 dims.
+//           Its A operand (lane l: row l%16, K = 4R..4R+3) is exactly the
+//           lane's p values. P goes in as two 16-bit parts, p_hi = p rounded
+//           and p_lo = (p - p_hi) rounded, so the products keep about 16 bits
+//           of p (one part alone keeps 8 for bf16, 11 for fp16); fp16 p is
+//           scaled by 2^7 first (p <= 2^15) so small weights stay normal.
+//           The B operand needs 4 consecutive tokens of one dim per lane:
+//           each wave writes its V block row-major to LDS and reads it back
+//           with ds_read_b64_tr_b16. That instruction (lane mapping checked
+//           on the GPU with an in-bounds probe) gives lane 16g+i the element
+//           i%4 of the 64-bit rows addressed by lanes 16g + i/4 + 4k,
+//           k = 0..3; so with lane 16g+j addressing V[token 4g + j/4][dims
+//           16c + 4(j%4) ..+3], lane 16g+i receives V[tokens 4g..4g+3][dim
+//           16c + i], the B operand of dims 16c..16c+15.
+// The output tile (lane l: columns 4R..4R+3, dim 16c + l%16) accumulates in
+// fp32 over all of the wave's blocks; the waves of the task are merged once
+// through LDS with the log-sum-exp rule.
+//
+// Against decode_mfma.hip (P.V on the VALU, 32*G FMAs per lane per block) the
+// vector work per block no longer grows with the group: at G = 8 that kernel
+// issues ~1.7x the VALU instructions of G = 4.
+#include "decode_tiled.h"
+
+namespace fd {
+
+namespace {
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+typedef s16x4 __attribute__((address_space(3))) * lds_s16x4_ptr;
+
+constexpr int kCols = 16;           // query heads per task
+constexpr float kLazyRescale = 8.f;  // log2 units
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_qk(const Vec8& a, const Vec8& b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma_qk<F16>(const Vec8& a, const Vec8& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_qk<BF16>(const Vec8& a, const Vec8& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_pv(s16x4 a, s16x4 b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma_pv<F16>(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4_t, a),
+                                               __builtin_bit_cast(f16x4_t, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma_pv<BF16>(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// p split into its 16-bit rounding and the rounding of the remainder.
+template <typename T>
+__device__ __forceinline__ void split16(float x, short& hi, short& lo) {
+  const uint16_t h = from_f32(T{}, x);
+  hi = (short)h;
+  lo = (short)from_f32(T{}, x - lo_f32(T{}, (uint32_t)h));
+}
+
+// LDS of one workgroup: the waves' V staging (two slots each) during the
+// block loop, then the waves' states for the merge.
+template <int D>
+struct __align__(16) MmLds {  // 16-byte V rows, float4 merge reads
+  static constexpr int kStage = 2 * kWavesPerTask * kTileTokens * D;  // 16-bit elements
+  struct Merge {
+    float acc[kWavesPerTask][kCols][D];
+    float m[kWavesPerTask][kCols];
+    float l[kWavesPerTask][kCols];
+    int bad[kWavesPerTask];
+  };
+  union {
+    uint16_t stage[kStage];
+    Merge merge;
+  };
+};
+
+template <typename T, int D, bool TWO>
+__global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledParams p) {
+  static_assert(D == 64 || D == 128, "decode_mm_kernel: head size 64 or 128");
+  constexpr int KS = D / 32;             // scores: 32-dim matrix-core steps
+  constexpr int NC = D / 16;             // P.V: 16-dim output chunks
+  constexpr int CPT = D / 8;             // V: 16-byte chunks per token row
+  constexpr int TPLD = kWave / CPT;      // V: tokens per load instruction
+  constexpr int NLD = kTileTokens / TPLD;  // V: loads per block
+  constexpr float kPScale = std::is_same<T, F16>::value ? 128.f : 1.f;
+
+  __shared__ MmLds<D> lds;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Task t;
+  if (!decode_task<kCols, TWO>(p, t)) return;
+  if (t.nb == 0 || t.range_bad) {
+    if (t.split == 0 && wave == 0) write_empty<T, D, kCols>(p, t, lane);
+    return;
+  }
+
+  const int col = lane & 15;  // K: token row of the A operand; scores: column
+  const int R = lane >> 4;    // K: dims 8R..+7 of each step; scores: tokens 4R..4R+3
+  const int vtok = lane / CPT;   // V: token of load 0 (load j: + TPLD*j)
+  const int vch = lane % CPT;    // V: 16-byte chunk of the token row
+
+  // B operand of the scores: column col's head, dims 8R + 32*ks .. +7
+  Vec8 qb[KS];
+  {
+    const uint16_t* qrow =
+        p.q + (int64_t)t.i * p.q_ss + (int64_t)task_head(t, col) * p.q_sh + R * 8;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) qb[ks] = ld16(qrow + 32 * ks);
+  }
+  // Byte offsets inside one (block, head) run, per tier: K step ks at
+  // koff + 64*ks; V load j at voff + j*vstep.
+  const TierParams& t0 = p.tier[0];
+  const uint32_t koff0 = (uint32_t)(((int64_t)col * t0.st + R * 8) * 2);
+  const uint32_t voff0 = (uint32_t)(((int64_t)vtok * t0.st + vch * 8) * 2);
+  const uint32_t vstep0 = (uint32_t)((int64_t)TPLD * t0.st * 2);
+  uint32_t koff1 = 0, voff1 = 0, vstep1 = 0;
+  if constexpr (TWO) {
+    const TierParams& t1 = p.tier[1];
+    koff1 = (uint32_t)(((int64_t)col * t1.st + R * 8) * 2);
+    voff1 = (uint32_t)(((int64_t)vtok * t1.st + vch * 8) * 2);
+    vstep1 = (uint32_t)((int64_t)TPLD * t1.st * 2);
+  }
+
+  // This wave's V staging, two slots of [16 tokens][D]; the tr16 read of
+  // chunk c by lane 16g+j starts at token 4g + j/4, dim 16c + 4(j%4).
+  uint16_t* stage = lds.stage + (wave * 2) * kTileTokens * D;
+  const int tr_off = (4 * R + (col >> 2)) * D + 4 * (col & 3);
+
+  // m: column col's running max (the same in the four rows); l: the sum of
+  // p over this lane's tokens; acc[c]: columns 4R..4R+3, dim 16c + col.
+  float m = neg_inf(), l = 0.f;
+  f32x4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const WaveBlocks wb = wave_blocks<TWO>(p, t, wave, lane);
+  const int nw = wb.nw;
+  auto ntok_of = [&](int k) -> int {
+    return block_tokens<TWO>(t, wb.first + kWavesPerTask * k);
+  };
+
+  // K single-buffered (free once the block's scores are computed), V
+  // double-buffered: block k+1's K and V are issued right after block k's
+  // scores and land while block k's softmax and P.V run.
+  Vec8 kb[KS], vb[2][NLD];
+  auto load_block = [&](int slot, int k) {
+    const BlockSrc src = block_src<TWO>(p, wb, t.kh, k);
+    const uint32_t koff = src.t1 ? koff1 : koff0;
+    const uint32_t voff = src.t1 ? voff1 : voff0;
+    const uint32_t vstep = src.t1 ? vstep1 : vstep0;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kb[ks] = buffer_ld16(src.k, koff, 64 * ks);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) vb[slot][j] = buffer_ld16(src.v, voff, j * vstep);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Scores of the resident K block (log2 domain, masked past ntok).
+  auto block_scores = [&](int ntok, float* s) {
+    f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) sv = mfma_qk<T>(kb[ks], qb[ks], sv);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = sv[r] * p.scale_log2;
+    if (ntok < kTileTokens) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = 4 * R + r < ntok ? s[r] : neg_inf();
+    }
+  };
+
+  // Softmax and P.V of the block whose scores are in s and V in vb[slot].
+  auto block_update = [&](int slot, int ntok, float* s) {
+    uint16_t* st = stage + slot * kTileTokens * D;
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      Vec8 x = vb[slot][j];
+      if (ntok < kTileTokens && vtok + TPLD * j >= ntok) x = Vec8{{0u, 0u, 0u, 0u}};  // stale V may be NaN
+      *reinterpret_cast<uint4*>(st + (vtok + TPLD * j) * D + vch * 8) =
+          make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
+    }
+    float bmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    bmax = fmaxf(bmax, shfl_xor_f32(bmax, 16));
+    bmax = fmaxf(bmax, shfl_xor_f32(bmax, 32));
+    const bool raise = bmax > m + kLazyRescale;  // false while both are -inf
+    if (__ballot(raise) != 0) {
+      const float mn = raise ? bmax : m;
+      const float alpha = raise ? fast_exp2(m - mn) : 1.f;  // 0 on the column's first raise
+      l *= alpha;
+      m = mn;
+      // acc row e holds column 4R + e, whose alpha lane 4R + e holds
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = __shfl(alpha, 4 * R + e, kWave);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[c][e] *= a;
+      }
+    }
+    const float ms = m == neg_inf() ? 0.f : m;
+    s16x4 phi, plo;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float pr = fast_exp2(s[r] - ms);
+      l += pr;
+      short h, lo;
+      split16<T>(pr * kPScale, h, lo);
+      phi[r] = h;
+      plo[r] = lo;
+    }
+    // the block's V rows are in LDS before any lane reads them transposed
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const s16x4 bv = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(st + tr_off + 16 * c));
+      acc[c] = mfma_pv<T>(phi, bv, acc[c]);
+      acc[c] = mfma_pv<T>(plo, bv, acc[c]);
+    }
+  };
+
+  // ---- main loop: two blocks per iteration (V slots ping-pong); loads in
+  // the steady-state body are unconditional so the wait counts only cover
+  // the block being reduced
+  if (nw > 0) {
+    float s[4];
+    int k = 0;
+    load_block(0, 0);
+    for (; k + 2 < nw; k += 2) {
+      block_scores(ntok_of(k), s);
+      load_block(1, k + 1);
+      block_update(0, ntok_of(k), s);
+      block_scores(ntok_of(k + 1), s);
+      load_block(0, k + 2);
+      block_update(1, ntok_of(k + 1), s);
+    }
+    block_scores(ntok_of(k), s);
+    if (k + 1 < nw) {
+      load_block(1, k + 1);
+      block_update(0, ntok_of(k), s);
+      block_scores(ntok_of(k + 1), s);
+      block_update(1, ntok_of(k + 1), s);
+    } else {
+      block_update(0, ntok_of(k), s);
+    }
+  }
+
+  // ---- this wave's state: column sums over the four rows (they share m),
+  // the output tile unscaled from the fp16 pre-scale
+  float lt = l + shfl_xor_f32(l, 16);
+  lt += shfl_xor_f32(lt, 32);
+  __syncthreads();  // every wave is done with its V staging (the merge reuses it)
+  auto& mg = lds.merge;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mg.acc[wave][4 * R + e][16 * c + col] = acc[c][e] * (1.f / kPScale);
+  }
+  if (lane < kCols) {
+    mg.m[wave][lane] = m;
+    mg.l[wave][lane] = lt;
+  }
+  if (lane == 0) mg.bad[wave] = wb.bad ? 1 : 0;
+  __syncthreads();
+
+  // ---- merge: wave w finishes columns w, w+4, w+8, w+12, each over LPC
+  // lanes of 8 dims
+  constexpr int LPC = D / 8;           // lanes per column
+  constexpr int CPP = kWave / LPC;     // columns per pass of the wave
+  bool bad = false;
+#pragma unroll
+  for (int w = 0; w < kWavesPerTask; ++w) bad |= mg.bad[w] != 0;
+  const bool write_final = t.nsplit == 1;
+#pragma unroll
+  for (int pass = 0; pass < (4 + CPP - 1) / CPP; ++pass) {
+    const int q = pass * CPP + lane / LPC;  // which of the wave's 4 columns
+    if (q >= 4) break;
+    const int cc = wave + 4 * q;
+    const int d0 = (lane % LPC) * 8;
+    float M = mg.m[0][cc];
+#pragma unroll
+    for (int w = 1; w < kWavesPerTask; ++w) M = fmaxf(M, mg.m[w][cc]);
+    const float Ms = M == neg_inf() ? 0.f : M;
+    float ltot = 0.f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWavesPerTask; ++w) {
+      const float sc = fast_exp2(mg.m[w][cc] - Ms);  // 0 for a wave without blocks
+      ltot += sc * mg.l[w][cc];
+      const float4 a = *reinterpret_cast<const float4*>(&mg.acc[w][cc][d0]);
+      const float4 b = *reinterpret_cast<const float4*>(&mg.acc[w][cc][d0 + 4]);
+      o[0] += sc * a.x;
+      o[1] += sc * a.y;
+      o[2] += sc * a.z;
+      o[3] += sc * a.w;
+      o[4] += sc * b.x;
+      o[5] += sc * b.y;
+      o[6] += sc * b.z;
+      o[7] += sc * b.w;
+    }
+    const float inv = 1.f / ltot;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= inv;
+    float lse_nat = (M + fast_log2(ltot)) * kLn2;
+    if (bad) {
+      lse_nat = qnan();
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = qnan();
+    }
+    if (cc < t.gcount && d0 < p.D) {
+      const int h = t.h0 + cc;
+      if (write_final) {
+        store8<T>(p.out, (int64_t)t.i * p.out_ss + (int64_t)h * p.out_sh + d0, p.out_f32, o);
+        if (d0 == 0) p.lse[(int64_t)h * p.lse_sh + t.i] = lse_nat;
+      } else {
+        const int64_t pidx = ((int64_t)t.i * p.H + h) * p.S + t.split;
+        store8<T>(p.part_o, pidx * p.D + d0, true, o);
+        if (d0 == 0) p.part_lse[pidx] = lse_nat;
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+hipError_t launch_d(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
+                    hipStream_t s) {
+  return two ? launch_capped(&decode_mm_kernel<T, D, true>, tp, tasks, sp, s)
+             : launch_capped(&decode_mm_kernel<T, D, false>, tp, tasks, sp, s);
+}
+
+template <typename T>
+hipError_t launch_t(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int D, bool two,
+                    hipStream_t s) {
+  switch (D) {
+    case 64: return launch_d<T, 64>(tp, tasks, sp, two, s);
+    case 128: return launch_d<T, 128>(tp, tasks, sp, two, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_mm(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
+                     int D, bool two_tiers, hipStream_t s) {
+  return kv_dtype == FD_F16 ? launch_t<F16>(tp, tasks, sp, D, two_tiers, s)
+                            : launch_t<BF16>(tp, tasks, sp, D, two_tiers, s);
+}
+
+}  // namespace fd

@@ -157,11 +157,17 @@ bool kv_adj_enabled() {
   return !(e != nullptr && strcmp(e, "0") == 0);
 }
 
-// FD_DECODE_KERNEL=valu keeps grouped-query calls on the VALU kernel
-// (comparison and tests); the matrix-core kernel is the default for G >= 4.
+// FD_DECODE_KERNEL=valu keeps grouped-query calls on the VALU kernel,
+// FD_DECODE_KERNEL=mfma on the kernel with only the scores on the matrix
+// cores (comparison and tests); by default groups of 4 take that kernel and
+// larger groups the one with P.V on the matrix cores too.
 bool valu_forced() {
   const char* e = getenv("FD_DECODE_KERNEL");
   return e != nullptr && strcmp(e, "valu") == 0;
+}
+bool mfma_forced() {
+  const char* e = getenv("FD_DECODE_KERNEL");
+  return e != nullptr && strcmp(e, "mfma") == 0;
 }
 
 }  // namespace
@@ -233,7 +239,7 @@ int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t
 }
 
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
-                      int32_t bt_width, int32_t kv_dtype, bool aligned) {
+                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix) {
   SplitPlan sp{};
   sp.passes = 1;
   const int G = KVH > 0 ? H / KVH : 0;
@@ -254,7 +260,15 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     sp.max_splits = 1;
     return sp;
   }
-  sp.mfma = G >= 4 && D == sp.kernel_d && !valu_forced();
+  sp.mfma = matrix && G >= 4 && D == sp.kernel_d && !valu_forced();
+  // groups of 5 and more: scores and P.V on the matrix cores, 16 query heads
+  // per task (at G = 8 the VALU P.V of the scores-only kernel issues ~1.7x
+  // the vector instructions of G = 4)
+  sp.mm = sp.mfma && G >= 5 && D <= 128 && !mfma_forced();
+  if (sp.mm) {
+    sp.mfma = false;
+    sp.kernel_g = 16;
+  }
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
   // tasks, splits and the model count 16-token tiles (BS / 16 per block)
   const int64_t tiles = (int64_t)(bt_width > 0 ? bt_width : 0) * (BS / kTileTokens);
@@ -358,8 +372,9 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
   const int G = sp.kernel_g;  // the kernel's head slots per task
-  hipError_t e = sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
-                         : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, sp.kernel_d, G, two, s);
+  hipError_t e = sp.mm     ? launch_mm(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s)
+                 : sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
+                           : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, sp.kernel_d, G, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");
   if (sp.max_splits > 1) {
     const int64_t threads = (int64_t)a.n * a.H * (a.D / 4);

@@ -82,11 +82,14 @@ struct TiledParams {
   int32_t split_blocks;
 };
 
-// Launchers of the two kernel families (decode_valu.hip, decode_mfma.hip).
+// Launchers of the kernel families (decode_valu.hip, decode_mfma.hip,
+// decode_mm.hip).
 hipError_t launch_valu(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
                        int D, int G, bool two_tiers, hipStream_t s);
 hipError_t launch_mfma(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
                        int D, int G, bool two_tiers, hipStream_t s);
+hipError_t launch_mm(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
+                     int D, bool two_tiers, hipStream_t s);
 
 // Dynamic LDS that caps `kernel` at two workgroups per CU (decode_partial.hip).
 unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache);
@@ -273,9 +276,7 @@ __device__ __forceinline__ void write_empty(const TiledParams& p, const Task& t,
   constexpr int LPT = D / 8;
   if (lane >= LPT || lane * 8 >= p.D) return;
   const float fill = t.range_bad ? qnan() : 0.f;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    if (g >= t.gcount) break;
+  for (int g = 0; g < t.gcount; ++g) {  // gcount <= G
     const int h = t.h0 + g;
     float o[8];
 #pragma unroll

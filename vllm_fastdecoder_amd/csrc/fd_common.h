@@ -184,16 +184,19 @@ struct SplitPlan {
   int32_t split_blocks;  // blocks handled by one wavefront task
   int32_t max_splits;    // ceil(bt_width / split_blocks)
   bool fast;             // the tiled kernel applies (else the generic one)
-  bool mfma;             // grouped-query scores on the matrix cores (G >= 4)
+  bool mfma;             // grouped-query scores on the matrix cores (G = 4, or 8 at D = 256)
+  bool mm;               // scores and P.V on the matrix cores (G >= 5, D <= 128)
   bool cap_occupancy;    // long tasks: at most two workgroups per CU
-  int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4 or 8
+  int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4, 8 or 16
   int32_t kernel_d;      // head size the tiled kernel is built for: 64, 128 or 256
   int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
                          // kernel_g), each over the same blocks
 };
 
+// matrix: the matrix-core kernels may be used (false when a tier lies in
+// pinned host memory, which the VALU kernel reads faster over the link).
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
-                      int32_t bt_width, int32_t kv_dtype, bool aligned);
+                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix = true);
 size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H,
                               int32_t D);
 int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s);
