@@ -95,7 +95,7 @@ def algorithmic_bytes(lens, n, H, KVH, D, BS, elt, out_elt):
 # The decode kernels' sources, hashed together to tie a committed counter
 # profile to the exact code it measured.
 KERNEL_SOURCES = ("fd_common.h", "decode_tiled.h", "decode_valu.hip", "decode_mfma.hip",
-                  "decode_mm.hip", "decode_partial.hip")
+                  "decode_mm.hip", "decode_f32.hip", "decode_partial.hip")
 
 
 def kernel_source_sha() -> str:

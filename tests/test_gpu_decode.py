@@ -227,10 +227,10 @@ GQA_LENS = [0, 1, 15, 16, 17, 93, 160, 47]
 @pytest.mark.parametrize("G", [4, 8])
 def test_gqa_kernels_match_oracle(gpu, kernel, dtype, D, G, monkeypatch):
     """Grouped-query rows (G = 4, 8) on each kernel: the default (scores on
-    the matrix cores at G = 4 and at D = 256; scores and P.V there at G = 8,
-    D <= 128), the scores-only matrix-core kernel (FD_DECODE_KERNEL=mfma) and
-    the VALU kernel (FD_DECODE_KERNEL=valu): lengths 0, 1, a partial block,
-    exactly one block, one token past it; whole rows and forced 2-block splits."""
+    the matrix cores at D = 256; scores and P.V there at D <= 128), the
+    scores-only matrix-core kernel (FD_DECODE_KERNEL=mfma) and the VALU
+    kernel (FD_DECODE_KERNEL=valu): lengths 0, 1, a partial block, exactly
+    one block, one token past it; whole rows and forced 2-block splits."""
     if kernel != "default":
         monkeypatch.setenv("FD_DECODE_KERNEL", kernel)
     KVH = 2
@@ -254,9 +254,13 @@ def test_gqa_kernels_match_oracle(gpu, kernel, dtype, D, G, monkeypatch):
         assert torch.equal(lse16, lse)
 
 
-def test_gqa_large_scores_and_range_errors(gpu):
-    """Matrix-core kernel: q x 300 stays finite and exact to the oracle; a bad
-    table entry or an over-long length poisons only its own row."""
+@pytest.mark.parametrize("kernel", ["default", "mfma"])
+def test_gqa_large_scores_and_range_errors(gpu, kernel, monkeypatch):
+    """Matrix-core kernels (both products there, the default; scores only):
+    q x 300 stays finite and exact to the oracle; a bad table entry or an
+    over-long length poisons only its own row."""
+    if kernel != "default":
+        monkeypatch.setenv("FD_DECODE_KERNEL", kernel)
     n, H, KVH, D, BS, C = 4, 16, 4, 128, 16, 16
     q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float32, 64, 9)
     q16 = (q * 300.0).to(torch.bfloat16)
@@ -460,7 +464,7 @@ def test_any_head_group_matches_oracle(gpu, kernel, H, KVH, D, dtype, monkeypatc
     """Query heads per kv head outside {1, 2, 4, 8}: 3 in a 4-slot kernel,
     5-7 in an 8-slot one (spare slots write nothing), 12, 16, 32 and
     multi-query as passes of up to 8 heads over the same blocks (16 on the
-    kernel with P.V on the matrix cores, the default for 5+ heads at D <= 128:
+    kernel with P.V on the matrix cores, the default for 4+ heads at D <= 128:
     27 = 16 + 11, 48 = 3 x 16). Host layout and vLLM's layout, whole rows and
     forced 2-block splits, lengths 0, 1, partial and whole blocks."""
     if kernel != "default":

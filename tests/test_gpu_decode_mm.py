@@ -1,5 +1,5 @@
 """GPU parity of the grouped-query kernel with both products on the matrix
-cores (decode_mm.hip: groups of 5 to 16 query heads per kv head in one pass,
+cores (decode_mm.hip: groups of 4 to 16 query heads per kv head in one pass,
 larger groups in passes of 16; head sizes 64 and 128; the default for those
 shapes in HBM) against the float64 oracle.
 
@@ -61,7 +61,7 @@ def _check(out, lse, ref_out, ref_lse, lens, dtype, gpu):
     assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
 
 
-@pytest.mark.parametrize("G", [5, 8, 12, 16, 20])
+@pytest.mark.parametrize("G", [4, 5, 8, 12, 16, 20])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_mm_kernel_matches_oracle(gpu, G, D, dtype, monkeypatch):
@@ -188,3 +188,23 @@ def test_mm_kernel_row_order_bit_identical(gpu):
         outs.append((out, lse))
     for out, lse in outs[1:]:
         assert torch.equal(out, outs[0][0]) and torch.equal(lse, outs[0][1])
+
+
+@pytest.mark.parametrize("G", [1, 2, 3])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mm_kernel_forced_on_small_groups(gpu, G, D, dtype, monkeypatch):
+    """FD_DECODE_KERNEL=mm on groups the planner gives the VALU kernel: 1-3
+    real heads in the 16 columns (the rest repeat the last head, unwritten);
+    whole rows and forced 2-block splits."""
+    monkeypatch.setenv("FD_DECODE_KERNEL", "mm")
+    KVH = 4
+    H = G * KVH
+    q, kc, vc, bt, lens = _case(H, KVH, D, dtype, seed=100 + G * D)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        for out_dtype in (torch.float32, dtype):
+            out, lse = run_host_layout(q, kc, vc, bt, lens, scale, out_dtype, gpu)
+            _check(out, lse, ref_out, ref_lse, lens, dtype, gpu)

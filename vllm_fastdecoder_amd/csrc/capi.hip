@@ -4,6 +4,8 @@
 // Every check runs before any launch, so a rejected call writes nothing
 // (the contract of fastdecode/csrc/cpu_attn.cpp:433-477 and :495-510, where
 // TORCH_CHECK raises before the kernel runs).
+#include <algorithm>
+
 #include <stdarg.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -104,7 +106,8 @@ int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_s
     aligned = aligned && kt.num_blocks > 0 && aligned16(kt.k) && aligned16(kt.v) &&
               kt.sb % 8 == 0 && kt.sh % 8 == 0 && kt.st % 8 == 0 &&
               // one (block, head) run must be addressable by a 32-bit offset
-              ((int64_t)(block_size - 1) * kt.st + head_size) * 2 < (1ll << 31);
+              ((int64_t)(block_size - 1) * kt.st + head_size) * (kv_dtype == FD_F32 ? 4 : 2) <
+                  (1ll << 31);
   }
   SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
                              (int32_t)width, kv_dtype, aligned);
@@ -163,16 +166,18 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || block_size <= 0 ||
       bt_width < 0)
     return set_error(FD_ERR_INVALID, "workspace_size: bad sizes");
-  // The aligned fast path is the only one that needs workspace; size for it,
-  // with or without the matrix-core kernels (a tier in pinned host memory
-  // takes the VALU kernel, whose head passes may split rows differently).
-  const SplitPlan a = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
-                                  FD_F16, true, true);
-  const SplitPlan b = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
-                                  FD_F16, true, false);
-  const size_t wa = decode_workspace_bytes(a, n, num_heads, head_size);
-  const size_t wb = decode_workspace_bytes(b, n, num_heads, head_size);
-  *bytes = wa > wb ? wa : wb;
+  // The aligned fast path is the only one that needs workspace; size for
+  // every kernel it may take (the kernels' head passes and the fp32 stream
+  // may split rows differently): 16-bit KV with or without the matrix-core
+  // kernels (a tier in pinned host memory takes the VALU kernel), fp32 KV.
+  size_t most = 0;
+  const int32_t dts[3] = {FD_F16, FD_F16, FD_F32};
+  for (int c = 0; c < 3; ++c) {
+    const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
+                                     dts[c], true, c == 0);
+    most = std::max(most, decode_workspace_bytes(sp, n, num_heads, head_size));
+  }
+  *bytes = most;
   return FD_OK;
 }
 

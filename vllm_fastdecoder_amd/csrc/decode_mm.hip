@@ -1,5 +1,5 @@
 // Grouped-query decode kernel with both products on the matrix cores, for
-// groups of 5 to 16 query heads per kv head (larger groups in passes of 16).
+// groups of 4 to 16 query heads per kv head (larger groups in passes of 16).
 //
 // Per 16-token block of one kv head and up to 16 of its query heads (the
 // "columns"; spare columns repeat the task's last head and are never

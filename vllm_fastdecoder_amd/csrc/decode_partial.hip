@@ -157,17 +157,13 @@ bool kv_adj_enabled() {
   return !(e != nullptr && strcmp(e, "0") == 0);
 }
 
-// FD_DECODE_KERNEL=valu keeps grouped-query calls on the VALU kernel,
-// FD_DECODE_KERNEL=mfma on the kernel with only the scores on the matrix
-// cores (comparison and tests); by default groups of 4 take that kernel and
-// larger groups the one with P.V on the matrix cores too.
-bool valu_forced() {
+// FD_DECODE_KERNEL=valu | mfma | mm forces a kernel family where it applies
+// (comparison and tests): the VALU kernel, the one with only the scores on
+// the matrix cores (4+ query heads per kv head), the one with P.V there too
+// (D <= 128).
+bool kernel_forced(const char* name) {
   const char* e = getenv("FD_DECODE_KERNEL");
-  return e != nullptr && strcmp(e, "valu") == 0;
-}
-bool mfma_forced() {
-  const char* e = getenv("FD_DECODE_KERNEL");
-  return e != nullptr && strcmp(e, "mfma") == 0;
+  return e != nullptr && strcmp(e, name) == 0;
 }
 
 }  // namespace
@@ -215,10 +211,10 @@ unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache) {
 // to measured launches of MHA and GQA-4 shapes at D = 128 (batch 1-64,
 // 128-16k tokens), where the choice lands within 4 % of the best split size.
 int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
-                           int32_t bt_width) {
+                           int32_t bt_width, int32_t elt) {
   constexpr double kWgRate = 50e9, kHbmRate = 6e12, kCombine = 8e-6, kFill = 0.5;
   const int64_t W = bt_width > 0 ? bt_width : 1;
-  const double blk = (double)BS * 2.0 * D * 2.0;  // K and V of one block, one kv head
+  const double blk = (double)BS * 2.0 * D * elt;  // K and V of one block, one kv head
   int32_t best = kMaxSplitBlocks;
   double best_t = 0.0;
   for (int32_t sb = kMaxSplitBlocks; sb >= 16; sb /= 2) {
@@ -243,28 +239,36 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   SplitPlan sp{};
   sp.passes = 1;
   const int G = KVH > 0 ? H / KVH : 0;
-  // The tiled kernels are built for 1, 2, 4 or 8 query heads per task: a
-  // group of 3 runs in a 4-head kernel, of 5-7 in an 8-head one (the spare
-  // head slots repeat a real head and write nothing), and more than 8 heads
-  // per kv head run as passes of up to 8, each re-reading the blocks.
-  sp.kernel_g = G <= 1 ? 1 : G == 2 ? 2 : G <= 4 ? 4 : 8;
+  // The tiled kernels are built for 1, 2, 4 or 8 query heads per task (16 on
+  // the matrix-core P.V kernel): a group of 3 runs in a 4-head kernel, of 5-7
+  // in an 8-head one (the spare head slots repeat a real head and write
+  // nothing), and more heads per kv head than a task holds run as passes,
+  // each re-reading the blocks.
+  const bool f32 = kv_dtype == FD_F32;
+  // (fp32 KV at D > 128: passes of 4, its 8-head kernel would spill)
+  sp.kernel_g = G <= 1 ? 1 : G == 2 ? 2 : (G <= 4 || (f32 && D > 128)) ? 4 : 8;
   // head sizes are built for 64, 128 and 256; any other multiple of 8 up to
   // 256 runs in the next larger one on the VALU kernel (its spare lanes idle)
   sp.kernel_d = D <= 64 ? 64 : D <= 128 ? 128 : 256;
   // cache blocks of 16 * m tokens are m 16-token tiles to the tiled kernels
   sp.fast = aligned && BS % kTileTokens == 0 && BS <= kMaxBlockSize && D % 8 == 0 && D >= 8 &&
             D <= 256 && G >= 1 &&
-            G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16);
+            G <= kMaxHeadGroup && (kv_dtype == FD_F16 || kv_dtype == FD_BF16 || f32);
   if (!sp.fast) {
     sp.split_blocks = bt_width > 0 ? bt_width : 1;
     sp.max_splits = 1;
     return sp;
   }
-  sp.mfma = matrix && G >= 4 && D == sp.kernel_d && !valu_forced();
-  // groups of 5 and more: scores and P.V on the matrix cores, 16 query heads
-  // per task (at G = 8 the VALU P.V of the scores-only kernel issues ~1.7x
-  // the vector instructions of G = 4)
-  sp.mm = sp.mfma && G >= 5 && D <= 128 && !mfma_forced();
+  // By default 4 and more query heads per kv head take the kernel with both
+  // products on the matrix cores at D <= 128 (16 query heads per task), the
+  // one with only the scores there at D = 256. Measured at n = 128, 8 kv
+  // heads, D = 128, bf16: G = 4 5.94 TB/s against 5.70 (scores only) and
+  // 5.77 (VALU); G = 8 5.9 against 5.2 and 3.0; below 4 heads the VALU
+  // kernel reads faster (G = 1 6.67, G = 3 6.09 against 5.98).
+  const bool matrix_ok = matrix && !f32 && D == sp.kernel_d && !kernel_forced("valu");
+  sp.mfma = matrix_ok && G >= 4;
+  sp.mm = matrix_ok && D <= 128 &&
+          (kernel_forced("mm") || (G >= 4 && !kernel_forced("mfma")));
   if (sp.mm) {
     sp.mfma = false;
     sp.kernel_g = 16;
@@ -276,7 +280,7 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   // each pass streams the blocks once more: model it as that many kv heads
-  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, kTileTokens, wt);
+  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, kTileTokens, wt, f32 ? 4 : 2);
   sp.split_blocks = sb;
   sp.max_splits = wt > 0 ? (wt + sb - 1) / sb : 1;
   const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=0: natural occupancy (tuning)
@@ -320,24 +324,28 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? FD_OK : hip_error(e, "decode_generic_kernel launch");
   }
+  // the tiled kernels address q and the caches in 16-bit words: an fp32
+  // element is two of them
+  const bool f32 = a.kv_dtype == FD_F32;
+  const int64_t ew = f32 ? 2 : 1;
   TiledParams tp{};
   tp.q = static_cast<const uint16_t*>(a.q);
-  tp.q_ss = a.q_ss;
-  tp.q_sh = a.q_sh;
+  tp.q_ss = a.q_ss * ew;
+  tp.q_sh = a.q_sh * ew;
   for (int t = 0; t < 2; ++t) {
     const KvTier& kt = a.tier[two ? t : 0];
     TierParams& tt = tp.tier[t];
     tt.k = static_cast<const uint16_t*>(kt.k);
     tt.v = static_cast<const uint16_t*>(kt.v);
-    tt.sb = kt.sb;
-    tt.sh = kt.sh;
-    tt.st = kt.st;
+    tt.sb = kt.sb * ew;
+    tt.sh = kt.sh * ew;
+    tt.st = kt.st * ew;
     tt.num_blocks = kt.num_blocks;
-    tt.run_bytes = (uint32_t)(((int64_t)(kTileTokens - 1) * kt.st + a.D) * 2);
+    tt.run_bytes = (uint32_t)(((int64_t)(kTileTokens - 1) * kt.st + a.D) * 2 * ew);
     // vLLM's cache keeps a token's V right after its K (v == k + D): the VALU
-    // kernel then reads both in one load (tier 0 only; the host tier of a
-    // split keeps separate K and V tensors).
-    tt.kv_adj = t == 0 && (a.D == 128 || a.D == 256) && kv_adj_enabled() &&
+    // kernel then reads both in one load (16-bit tier 0 only; the host tier
+    // of a split keeps separate K and V tensors).
+    tt.kv_adj = t == 0 && !f32 && (a.D == 128 || a.D == 256) && kv_adj_enabled() &&
                 static_cast<const char*>(kt.v) == static_cast<const char*>(kt.k) + (int64_t)a.D * 2;
     tt.k_run_bytes = tt.run_bytes + (tt.kv_adj ? (uint32_t)a.D * 2 : 0u);
     tt.bt = kt.bt;
@@ -372,7 +380,8 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
   const int G = sp.kernel_g;  // the kernel's head slots per task
-  hipError_t e = sp.mm     ? launch_mm(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s)
+  hipError_t e = f32       ? launch_f32(tp, (unsigned)tasks, sp, sp.kernel_d, G, two, s)
+                 : sp.mm   ? launch_mm(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s)
                  : sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
                            : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, sp.kernel_d, G, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");

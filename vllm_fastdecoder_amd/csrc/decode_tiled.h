@@ -83,13 +83,15 @@ struct TiledParams {
 };
 
 // Launchers of the kernel families (decode_valu.hip, decode_mfma.hip,
-// decode_mm.hip).
+// decode_mm.hip, decode_f32.hip).
 hipError_t launch_valu(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
                        int D, int G, bool two_tiers, hipStream_t s);
 hipError_t launch_mfma(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
                        int D, int G, bool two_tiers, hipStream_t s);
 hipError_t launch_mm(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int kv_dtype,
                      int D, bool two_tiers, hipStream_t s);
+hipError_t launch_f32(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int D, int G,
+                      bool two_tiers, hipStream_t s);
 
 // Dynamic LDS that caps `kernel` at two workgroups per CU (decode_partial.hip).
 unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache);
@@ -188,14 +190,15 @@ __device__ __forceinline__ void axpy8(float p, const Vec8& v, float* acc) {
   }
 }
 
-// Writes 8 consecutive outputs starting at element `off` of `out`.
+// Writes 8 consecutive outputs starting at element `off` of `out` (fp32
+// when `f32` is set or the KV is fp32, else the 16-bit KV type).
 template <typename T>
 __device__ __forceinline__ void store8(void* out, int64_t off, bool f32, const float* o) {
-  if (f32) {
+  if (std::is_same<T, F32>::value || f32) {
     float4* p = reinterpret_cast<float4*>(static_cast<float*>(out) + off);
     p[0] = make_float4(o[0], o[1], o[2], o[3]);
     p[1] = make_float4(o[4], o[5], o[6], o[7]);
-  } else {
+  } else if constexpr (!std::is_same<T, F32>::value) {
     uint4 u;
     u.x = from_f32(T{}, o[0]) | (uint32_t(from_f32(T{}, o[1])) << 16);
     u.y = from_f32(T{}, o[2]) | (uint32_t(from_f32(T{}, o[3])) << 16);
@@ -341,6 +344,45 @@ struct WaveStates {
   float l[kWavesPerTask][G];
   int bad[kWavesPerTask];
 };
+
+// Folds the TPW = 64 / LPT lane-rows of a wave (each with its own softmax
+// state per head: log2-domain max m, sum l, accumulator of its 8 dims) into
+// the wave's state and publishes it in `ws` for finish_task.
+template <int D, int G>
+__device__ __forceinline__ void publish_wave_state(WaveStates<D, G>& ws, int wave, int lane,
+                                                   const float* m, const float* l,
+                                                   const float (*acc)[8], bool bad) {
+  constexpr int LPT = D / 8;
+  const int chunk = lane % LPT;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = m[g];
+#pragma unroll
+    for (int x = LPT; x < kWave; x <<= 1) M = fmaxf(M, shfl_xor_f32(M, x));
+    const float Ms = M == neg_inf() ? 0.f : M;
+    const float w = fast_exp2(m[g] - Ms);
+    float lt = l[g] * w;
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = acc[g][e] * w;
+#pragma unroll
+    for (int x = LPT; x < kWave; x <<= 1) {
+      lt += shfl_xor_f32(lt, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] += shfl_xor_f32(o[e], x);
+    }
+    if (lane < LPT) {
+      float4* dst = reinterpret_cast<float4*>(&ws.acc[wave][g][chunk * 8]);
+      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+    }
+    if (lane == 0) {
+      ws.m[wave][g] = M;
+      ws.l[wave][g] = lt;
+    }
+  }
+  if (lane == 0) ws.bad[wave] = bad ? 1 : 0;
+}
 
 // Wave 0, after the workgroup barrier: merges the waves' states with the
 // log-sum-exp rule and writes the final result (one split) or this split's

@@ -194,34 +194,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   }
 
   // ---- merge the TPW lane-rows of each head into this wave's state, publish it
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float M = m[g];
-#pragma unroll
-    for (int x = LPT; x < kWave; x <<= 1) M = fmaxf(M, shfl_xor_f32(M, x));
-    const float Ms = M == neg_inf() ? 0.f : M;
-    const float w = fast_exp2(m[g] - Ms);
-    float lt = l[g] * w;
-    float o[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = acc[g][e] * w;
-#pragma unroll
-    for (int x = LPT; x < kWave; x <<= 1) {
-      lt += shfl_xor_f32(lt, x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += shfl_xor_f32(o[e], x);
-    }
-    if (lane < LPT) {
-      float4* dst = reinterpret_cast<float4*>(&ws.acc[wave][g][chunk * 8]);
-      dst[0] = make_float4(o[0], o[1], o[2], o[3]);
-      dst[1] = make_float4(o[4], o[5], o[6], o[7]);
-    }
-    if (lane == 0) {
-      ws.m[wave][g] = M;
-      ws.l[wave][g] = lt;
-    }
-  }
-  if (lane == 0) ws.bad[wave] = wb.bad ? 1 : 0;
+  publish_wave_state<D, G>(ws, wave, lane, m, l, acc, wb.bad);
   __syncthreads();
   if (wave != 0) return;
   finish_task<T, D, G>(p, t, ws, lane);

@@ -37,6 +37,10 @@ struct F16 {
 struct BF16 {
   static constexpr int kCode = FD_BF16;
 };
+// fp32 KV (its outputs are always fp32).
+struct F32 {
+  static constexpr int kCode = FD_F32;
+};
 
 // Low / high 16-bit element of a packed 32-bit word as fp32.
 __device__ __forceinline__ float lo_f32(F16, uint32_t w) {
@@ -184,8 +188,8 @@ struct SplitPlan {
   int32_t split_blocks;  // blocks handled by one wavefront task
   int32_t max_splits;    // ceil(bt_width / split_blocks)
   bool fast;             // the tiled kernel applies (else the generic one)
-  bool mfma;             // grouped-query scores on the matrix cores (G = 4, or 8 at D = 256)
-  bool mm;               // scores and P.V on the matrix cores (G >= 5, D <= 128)
+  bool mfma;             // grouped-query scores on the matrix cores (G >= 4 at D = 256)
+  bool mm;               // scores and P.V on the matrix cores (G >= 4, D <= 128)
   bool cap_occupancy;    // long tasks: at most two workgroups per CU
   int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4, 8 or 16
   int32_t kernel_d;      // head size the tiled kernel is built for: 64, 128 or 256
