@@ -408,7 +408,7 @@ def traffic_record(name: str, layout: str):
         else None
 
 
-def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False):
+def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False, min_warm_ms=0.0):
     """Times one paged partial decode over every row's blocks of workload w,
     all in HBM, rows scheduled longest first. copies > 1: that many copies of
     the pool, launch k reading copy k % copies, so that a pool smaller than
@@ -416,8 +416,9 @@ def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False):
     the small-batch pool is 268 MB). graph: the timed launches are captured
     in one HIP graph and replayed, as a serving engine issues its decode
     step, so that Python's per-call overhead does not pad launches of a few
-    microseconds. Returns (ms per launch, algorithmic bytes, K+V bytes,
-    lens, timing note)."""
+    microseconds. min_warm_ms: the warm-up also lasts at least that long
+    (the GPU's clocks settle over the first ~30 ms of launches). Returns (ms
+    per launch, algorithmic bytes, K+V bytes, lens, timing note)."""
     import torch
 
     from tests import cases
@@ -441,10 +442,20 @@ def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False):
             ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse, row_order=order_d)
 
     nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    warm = ""
+    if min_warm_ms > 0:
+        t0, k = time.perf_counter(), 0
+        while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+            launch(k)
+            k += 1
+            if k % 8 == 0:
+                torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        warm = f" (and at least {min_warm_ms:.0f} ms of launches before them)"
     if not graph:
         counter = iter(range(1 << 62))
         ms = time_gpu(lambda: launch(next(counter)), steps, warmup, stream)
-        note = f"HIP events around {steps} launches after {warmup} warm-ups"
+        note = f"HIP events around {steps} launches after {warmup} warm-ups{warm}"
         return ms, nbytes, kvb, lens, note
     for k in range(warmup):
         launch(k)
@@ -467,7 +478,7 @@ def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False):
     end.synchronize()
     ms = start.elapsed_time(end) / (replays * steps)
     note = (f"one HIP graph of {steps} launches over {copies} pool copies, HIP events around "
-            f"{replays} replays after {warmup} eager warm-ups")
+            f"{replays} replays after {warmup} eager warm-ups{warm}")
     del g, pools
     return ms, nbytes, kvb, lens, note
 
@@ -522,14 +533,15 @@ def main() -> int:
         return 0
     # Legs run first, in this order: the small-batch shape (pool copies
     # rotated past the Infinity Cache, launches replayed from a HIP graph) and
-    # the Llama-3-8B grouped-query shape, each with its own roofline; then the
-    # headline shape.
+    # the Llama-3-8B grouped-query shape, each with its own roofline and at
+    # least 100 ms of warm-up launches (steady clocks, as in a serving loop);
+    # then the headline shape, after exactly --warmup launches.
     legs = {}
     if args.workload == "vicuna7b" and not args.no_legs:
         for name, copies, graph in (("correctness", 5, True), ("llama3_8b", 1, False)):
             lw = cases.WORKLOADS[name]
             ms_l, nb_l, kv_l, _, note = decode_leg(lw, "vllm", args.steps, args.warmup, dev,
-                                                  copies=copies, graph=graph)
+                                                  copies=copies, graph=graph, min_warm_ms=100.0)
             key = "small_batch_leg" if name == "correctness" else "llama3_8b_leg"
             legs[key] = leg_summary(lw, "vllm", ms_l, nb_l, kv_l, note, copies=copies)
             torch.cuda.empty_cache()

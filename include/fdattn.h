@@ -131,8 +131,11 @@ int fd_paged_decode_partial(
     void* stream);
 
 /* Bytes of workspace fd_paged_decode_partial needs for these sizes (the
- * block-range split partials). No counterpart in the reference: its CPU
- * kernel keeps per-thread scratch in std::vector (cpu_attn.cpp:314-318). */
+ * block-range split partials), whatever the kv dtype and wherever the cache
+ * lies: the largest need of the kernels such a call may take (an fp32 cache
+ * streams twice the bytes per block and may split rows sooner). No
+ * counterpart in the reference: its CPU kernel keeps per-thread scratch in
+ * std::vector (cpu_attn.cpp:314-318). */
 int fd_paged_decode_workspace_size(
     int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
     int32_t block_size, int32_t bt_width, size_t* bytes);

@@ -65,8 +65,10 @@ def test_paged_decode_in_a_graph(gpu, split, monkeypatch):
     def step():
         ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse)
 
+    # an upper bound over the kernels this shape may take; forced 2-block
+    # tasks always split these rows
     ws = ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1])
-    assert (ws > 0) == (split == "2")
+    assert ws > 0 or split != "2"
     _replays(gpu, q, step, [out, lse], ws_bytes=ws)
 
 
