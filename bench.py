@@ -408,79 +408,109 @@ def traffic_record(name: str, layout: str):
         else None
 
 
-def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False, min_warm_ms=0.0):
-    """Times one paged partial decode over every row's blocks of workload w,
-    all in HBM, rows scheduled longest first. copies > 1: that many copies of
-    the pool, launch k reading copy k % copies, so that a pool smaller than
-    the 256 MB Infinity Cache is not served from it on repeats (each copy of
-    the small-batch pool is 268 MB). graph: the timed launches are captured
-    in one HIP graph and replayed, as a serving engine issues its decode
-    step, so that Python's per-call overhead does not pad launches of a few
-    microseconds. min_warm_ms: the warm-up also lasts at least that long
-    (the GPU's clocks settle over the first ~30 ms of launches). Returns (ms
-    per launch, algorithmic bytes, K+V bytes, lens, timing note)."""
-    import torch
+class DecodeLeg:
+    """One paged partial decode over every row's blocks of workload w, all in
+    HBM, rows scheduled longest first, with its inputs built (and resident)
+    at construction. copies > 1: that many copies of the pool, launch k
+    reading copy k % copies, so that a pool smaller than the 256 MB Infinity
+    Cache is not served from it on repeats (each copy of the small-batch pool
+    is 268 MB)."""
 
-    from tests import cases
-    from vllm_fastdecoder_amd import ops
+    def __init__(self, w, layout, dev, copies=1):
+        import torch
 
-    lens, bt, pool = cases.draw_lens_and_tables(w)
-    pools = [cases.kv_pool(w, pool, layout, dev, seed_offset=c) for c in range(copies)]
-    q = cases.queries(w, dev)
-    bt_d, lens_d = bt.to(dev), lens.to(dev)
-    order_d = ops.longest_first(lens).to(dev)
-    out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
-    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
-    stream = torch.cuda.current_stream(dev)
+        from tests import cases
+        from vllm_fastdecoder_amd import ops
 
-    def launch(k):
-        kc, vc, _ = pools[k % copies]
-        if layout == "vllm":
-            ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse,
-                             row_order=order_d)
-        else:
-            ops.decode_attn(q, kc, vc, bt_d, lens_d, w.scale, out, lse, row_order=order_d)
-
-    nbytes, kvb = algorithmic_bytes(lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
-    warm = ""
-    if min_warm_ms > 0:
-        t0, k = time.perf_counter(), 0
-        while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
-            launch(k)
-            k += 1
-            if k % 8 == 0:
-                torch.cuda.synchronize()
+        self.w, self.layout, self.dev, self.copies = w, layout, dev, copies
+        self.lens, self.bt, pool = cases.draw_lens_and_tables(w)
+        self.pools = [cases.kv_pool(w, pool, layout, dev, seed_offset=c) for c in range(copies)]
+        self.q = cases.queries(w, dev)
+        self.bt_d, self.lens_d = self.bt.to(dev), self.lens.to(dev)
+        self.order_d = ops.longest_first(self.lens).to(dev)
+        self.out = torch.empty(w.n, w.H, w.D, dtype=w.dtype, device=dev)
+        self.lse = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
+        self.nbytes, self.kvb = algorithmic_bytes(self.lens, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
         torch.cuda.synchronize()
-        warm = f" (and at least {min_warm_ms:.0f} ms of launches before them)"
-    if not graph:
-        counter = iter(range(1 << 62))
-        ms = time_gpu(lambda: launch(next(counter)), steps, warmup, stream)
-        note = f"HIP events around {steps} launches after {warmup} warm-ups{warm}"
-        return ms, nbytes, kvb, lens, note
-    for k in range(warmup):
-        launch(k)
-    torch.cuda.synchronize()
-    side = torch.cuda.Stream(device=dev)
-    ops.reserve_workspace(side, ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1]))
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=side):
-        for k in range(steps):
-            launch(k)
-    replays = 10
-    g.replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(replays):
+
+    def launch(self, k):
+        from vllm_fastdecoder_amd import ops
+
+        kc, vc, _ = self.pools[k % self.copies]
+        w = self.w
+        if self.layout == "vllm":
+            ops.paged_decode(self.q, kc, vc, self.bt_d, self.lens_d, w.scale, out=self.out,
+                             lse=self.lse, row_order=self.order_d)
+        else:
+            ops.decode_attn(self.q, kc, vc, self.bt_d, self.lens_d, w.scale, self.out, self.lse,
+                            row_order=self.order_d)
+
+    def time(self, steps, warmup, graph=False, min_warm_ms=0.0):
+        """warmup untimed launches, then `steps` timed ones (HIP events on the
+        launch stream). graph: the timed launches are captured in one HIP
+        graph and replayed, as a serving engine issues its decode step, so
+        that Python's per-call overhead does not pad launches of a few
+        microseconds. min_warm_ms: the warm-up also lasts at least that long
+        (the GPU's clocks settle over the first ~30 ms of launches). Returns
+        (ms per launch, algorithmic bytes, K+V bytes, lens, timing note)."""
+        import torch
+
+        from vllm_fastdecoder_amd import ops
+
+        w, dev = self.w, self.dev
+        stream = torch.cuda.current_stream(dev)
+        warm = ""
+        if min_warm_ms > 0:
+            t0, k = time.perf_counter(), 0
+            while (time.perf_counter() - t0) * 1e3 < min_warm_ms:
+                self.launch(k)
+                k += 1
+                if k % 8 == 0:
+                    torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            warm = f" (and at least {min_warm_ms:.0f} ms of launches before them)"
+        if not graph:
+            counter = iter(range(1 << 62))
+            ms = time_gpu(lambda: self.launch(next(counter)), steps, warmup, stream)
+            note = f"HIP events around {steps} launches after {warmup} warm-ups{warm}"
+            return ms, self.nbytes, self.kvb, self.lens, note
+        for k in range(warmup):
+            self.launch(k)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream(device=dev)
+        ops.reserve_workspace(side, ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS,
+                                                        self.bt.shape[1]))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            for k in range(steps):
+                self.launch(k)
+        replays = 10
         g.replay()
-    end.record(stream)
-    end.synchronize()
-    ms = start.elapsed_time(end) / (replays * steps)
-    note = (f"one HIP graph of {steps} launches over {copies} pool copies, HIP events around "
-            f"{replays} replays after {warmup} eager warm-ups{warm}")
-    del g, pools
-    return ms, nbytes, kvb, lens, note
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            g.replay()
+        end.record(stream)
+        end.synchronize()
+        ms = start.elapsed_time(end) / (replays * steps)
+        note = (f"one HIP graph of {steps} launches over {self.copies} pool copies, HIP events "
+                f"around {replays} replays after {warmup} eager warm-ups{warm}")
+        del g
+        return ms, self.nbytes, self.kvb, self.lens, note
+
+    def release(self):
+        self.pools = None
+
+
+def decode_leg(w, layout, steps, warmup, dev, copies=1, graph=False, min_warm_ms=0.0):
+    """DecodeLeg(w, layout, dev, copies).time(steps, warmup, graph, min_warm_ms)."""
+    leg = DecodeLeg(w, layout, dev, copies)
+    try:
+        return leg.time(steps, warmup, graph=graph, min_warm_ms=min_warm_ms)
+    finally:
+        leg.release()
 
 
 def leg_summary(w, layout, ms, nbytes, kvb, note, copies=1):
@@ -531,23 +561,28 @@ def main() -> int:
         print(json.dumps(hybrid_profile(w, lens, bt, cases.queries(w, dev), args.hybrid_profile,
                                         args.steps, args.warmup, torch.cuda.current_stream(dev))))
         return 0
-    # Legs run first, in this order: the small-batch shape (pool copies
-    # rotated past the Infinity Cache, launches replayed from a HIP graph) and
-    # the Llama-3-8B grouped-query shape, each with its own roofline and at
-    # least 100 ms of warm-up launches (steady clocks, as in a serving loop);
-    # then the headline shape, after exactly --warmup launches.
+    # The headline's inputs are built first. Then the legs run, in this order:
+    # the small-batch shape (pool copies rotated past the Infinity Cache,
+    # launches replayed from a HIP graph) and the Llama-3-8B grouped-query
+    # shape, each with its own roofline and at least 100 ms of warm-up
+    # launches (steady clocks, as in a serving loop); then the headline, after
+    # exactly --warmup launches, with no idle gap or input generation between
+    # the last leg's launches and its own (a GPU left idle, or filling a pool,
+    # reads a few % slower for tens of launches afterwards).
+    copies = args.copies if args.copies is not None else (5 if w.name == "correctness" else 1)
+    head = DecodeLeg(w, args.layout, dev, copies=copies)
     legs = {}
     if args.workload == "vicuna7b" and not args.no_legs:
-        for name, copies, graph in (("correctness", 5, True), ("llama3_8b", 1, False)):
+        for name, lcopies, graph in (("correctness", 5, True), ("llama3_8b", 1, False)):
             lw = cases.WORKLOADS[name]
             ms_l, nb_l, kv_l, _, note = decode_leg(lw, "vllm", args.steps, args.warmup, dev,
-                                                  copies=copies, graph=graph, min_warm_ms=100.0)
+                                                  copies=lcopies, graph=graph, min_warm_ms=100.0)
             key = "small_batch_leg" if name == "correctness" else "llama3_8b_leg"
-            legs[key] = leg_summary(lw, "vllm", ms_l, nb_l, kv_l, note, copies=copies)
-            torch.cuda.empty_cache()
-    copies = args.copies if args.copies is not None else (5 if w.name == "correctness" else 1)
-    ms, nbytes, kvb, _, timing = decode_leg(w, args.layout, args.steps, args.warmup, dev,
-                                            copies=copies, graph=w.name == "correctness")
+            legs[key] = leg_summary(lw, "vllm", ms_l, nb_l, kv_l, note, copies=lcopies)
+    ms, nbytes, kvb, _, timing = head.time(args.steps, args.warmup,
+                                           graph=w.name == "correctness")
+    head.release()
+    torch.cuda.empty_cache()
     gbps = nbytes / (ms / 1e3) / 1e9
     traffic = traffic_record(w.name, args.layout)
     q = cases.queries(w, dev)

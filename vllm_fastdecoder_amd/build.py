@@ -33,6 +33,15 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions. decode_mm.hip: MFMA accumulators in VGPRs. With the
+# default heuristic its P.V accumulators live in AGPRs, and the rarely taken
+# rescale branch of every block makes the compiler copy all 32 of them to
+# VGPRs and back on the common path too (64 v_accvgpr moves per block); in
+# VGPRs the kernel needs 154 registers and no AGPRs.
+SOURCE_FLAGS = {
+    "decode_mm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
 CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wno-unused-function"]
 
 
@@ -79,8 +88,8 @@ def build(verbose: bool = False, out: Path | None = None) -> Path:
     with tempfile.TemporaryDirectory(prefix="fdattn_build_") as d:
         objs = [Path(d) / (src.stem + ".o") for src in srcs]
         hobjs = [Path(d) / (src.stem + ".host.o") for src in hsrcs]
-        cmds = [[hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
-                for src, obj in zip(srcs, objs)]
+        cmds = [[hipcc(), *HIPCC_FLAGS, *SOURCE_FLAGS.get(src.name, []), "-c", str(src), "-o",
+                 str(obj)] for src, obj in zip(srcs, objs)]
         cmds += [[cxx(), *CXX_FLAGS, "-c", str(src), "-o", str(obj)]
                  for src, obj in zip(hsrcs, hobjs)]
         with ThreadPoolExecutor(max_workers=jobs) as pool:

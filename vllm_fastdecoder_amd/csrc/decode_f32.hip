@@ -189,8 +189,8 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(Tiled
 template <int D, int G>
 hipError_t launch_dg(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
                      hipStream_t s) {
-  return two ? launch_capped(&decode_f32_kernel<D, G, true>, tp, tasks, sp, s)
-             : launch_capped(&decode_f32_kernel<D, G, false>, tp, tasks, sp, s);
+  return two ? launch_capped<&decode_f32_kernel<D, G, true>>(tp, tasks, sp, s)
+             : launch_capped<&decode_f32_kernel<D, G, false>>(tp, tasks, sp, s);
 }
 
 template <int D>

@@ -291,8 +291,8 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
 template <typename T, int D, int G>
 hipError_t launch_dg(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
                      hipStream_t s) {
-  return two ? launch_capped(&decode_mfma_kernel<T, D, G, true>, tp, tasks, sp, s)
-             : launch_capped(&decode_mfma_kernel<T, D, G, false>, tp, tasks, sp, s);
+  return two ? launch_capped<&decode_mfma_kernel<T, D, G, true>>(tp, tasks, sp, s)
+             : launch_capped<&decode_mfma_kernel<T, D, G, false>>(tp, tasks, sp, s);
 }
 
 template <typename T, int D>

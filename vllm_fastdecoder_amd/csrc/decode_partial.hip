@@ -168,6 +168,20 @@ bool kernel_forced(const char* name) {
 
 }  // namespace
 
+// Compute units of the current device (cached per device; 0 if unknown).
+static int device_cus() {
+  static std::atomic<int> cache[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  const int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v - 1;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    cus = 0;
+  cache[dev].store(cus + 1, std::memory_order_relaxed);
+  return cus;
+}
+
 // Dynamic LDS that leaves room for at most two workgroups of `kernel` per CU
 // (the reservation is never touched), or 0 when the kernel's own LDS already
 // keeps it there or the reservation would not fit one workgroup's limit.
@@ -259,24 +273,35 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     sp.max_splits = 1;
     return sp;
   }
-  // By default 4 and more query heads per kv head take the kernel with both
-  // products on the matrix cores at D <= 128 (16 query heads per task), the
-  // one with only the scores there at D = 256. Measured at n = 128, 8 kv
-  // heads, D = 128, bf16: G = 4 5.94 TB/s against 5.70 (scores only) and
-  // 5.77 (VALU); G = 8 5.9 against 5.2 and 3.0; below 4 heads the VALU
-  // kernel reads faster (G = 1 6.67, G = 3 6.09 against 5.98).
+  // tasks, splits and the model count 16-token tiles (BS / 16 per block)
+  const int64_t tiles = (int64_t)(bt_width > 0 ? bt_width : 0) * (BS / kTileTokens);
+  const int32_t wt = (int32_t)std::min<int64_t>(tiles, INT32_MAX);
+  // Kernel family (one box, vLLM layout, rows longest first, D = 128):
+  //   * 4 and more query heads per kv head take the kernel with both
+  //     products on the matrix cores at D <= 128 (16 query heads per task),
+  //     the one with only the scores there at D = 256. At n = 64 / 256, 8 kv
+  //     heads, bf16: G = 4 5.88 / 6.81 TB/s against 5.76 / 6.75 (scores
+  //     only) and 5.67 / 6.79 (VALU); G = 8 5.48 / 6.64 against 4.88 / 6.12
+  //     and 2.86 / 3.08.
+  //   * MHA at D = 128 takes it too on large launches: with >= 8 tasks per
+  //     CU and rows that may reach 1,024 tokens it reads 0.5-1.3 % faster
+  //     than the VALU kernel (n = 64-256 x 32 heads, fp16 / bf16, L in
+  //     [256, 2048] or [1024, 4096]); with fewer tasks its longer per-block
+  //     chain loses (n = 32: -3 %), and so it does on short rows (L <= 512:
+  //     -1 %). G = 2 / 3 and D = 64 stay on the VALU kernel (G = 2, n = 128:
+  //     6.79 against 6.74 TB/s; MHA D = 64: 6.50 against 6.03).
   const bool matrix_ok = matrix && !f32 && D == sp.kernel_d && !kernel_forced("valu");
+  const int cus = device_cus();
+  const bool big_mha = G == 1 && D == 128 && cus > 0 && (int64_t)n * KVH >= 8LL * cus &&
+                       wt >= 1024 / kTileTokens;
   sp.mfma = matrix_ok && G >= 4;
   sp.mm = matrix_ok && D <= 128 &&
-          (kernel_forced("mm") || (G >= 4 && !kernel_forced("mfma")));
+          (kernel_forced("mm") || ((G >= 4 || big_mha) && !kernel_forced("mfma")));
   if (sp.mm) {
     sp.mfma = false;
     sp.kernel_g = 16;
   }
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
-  // tasks, splits and the model count 16-token tiles (BS / 16 per block)
-  const int64_t tiles = (int64_t)(bt_width > 0 ? bt_width : 0) * (BS / kTileTokens);
-  const int32_t wt = (int32_t)std::min<int64_t>(tiles, INT32_MAX);
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   // each pass streams the blocks once more: model it as that many kv heads

@@ -96,15 +96,18 @@ hipError_t launch_f32(const TiledParams& tp, unsigned tasks, const SplitPlan& sp
 // Dynamic LDS that caps `kernel` at two workgroups per CU (decode_partial.hip).
 unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache);
 
-// Launches `kernel` with the occupancy cap when the plan asks for it; one
-// settings cache per kernel instantiation.
-template <typename Kernel>
-hipError_t launch_capped(Kernel kernel, const TiledParams& tp, unsigned tasks,
-                         const SplitPlan& sp, hipStream_t s) {
+// Launches `Kernel` with the occupancy cap when the plan asks for it. The
+// kernel is a template argument so that each kernel has its own settings
+// cache: the reserve depends on the kernel's static LDS (every kernel here
+// has the type void(TiledParams), so a cache keyed by the pointer's type
+// would hand the first kernel's reserve to all the others).
+template <void (*Kernel)(TiledParams)>
+hipError_t launch_capped(const TiledParams& tp, unsigned tasks, const SplitPlan& sp,
+                         hipStream_t s) {
   static std::atomic<int> cache[kMaxDevices] = {};
   const unsigned lds =
-      sp.cap_occupancy ? two_per_cu_lds(reinterpret_cast<const void*>(kernel), cache) : 0;
-  hipLaunchKernelGGL(kernel, dim3(tasks), dim3(kWave * kWavesPerTask), lds, s, tp);
+      sp.cap_occupancy ? two_per_cu_lds(reinterpret_cast<const void*>(Kernel), cache) : 0;
+  hipLaunchKernelGGL(Kernel, dim3(tasks), dim3(kWave * kWavesPerTask), lds, s, tp);
   return hipGetLastError();
 }
 

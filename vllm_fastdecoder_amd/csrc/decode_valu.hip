@@ -205,11 +205,11 @@ hipError_t launch_dg(const TiledParams& tp, unsigned tasks, const SplitPlan& sp,
                      hipStream_t s) {
   if constexpr (D == 128 || D == 256) {
     if (tp.tier[0].kv_adj)
-      return two ? launch_capped(&decode_tiled_kernel<T, D, G, true, true>, tp, tasks, sp, s)
-                 : launch_capped(&decode_tiled_kernel<T, D, G, false, true>, tp, tasks, sp, s);
+      return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, true>>(tp, tasks, sp, s)
+                 : launch_capped<&decode_tiled_kernel<T, D, G, false, true>>(tp, tasks, sp, s);
   }
-  return two ? launch_capped(&decode_tiled_kernel<T, D, G, true, false>, tp, tasks, sp, s)
-             : launch_capped(&decode_tiled_kernel<T, D, G, false, false>, tp, tasks, sp, s);
+  return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, false>>(tp, tasks, sp, s)
+             : launch_capped<&decode_tiled_kernel<T, D, G, false, false>>(tp, tasks, sp, s);
 }
 
 template <typename T, int D>
