@@ -1,7 +1,7 @@
 """GPU parity of the grouped-query kernel with both products on the matrix
 cores (decode_mm.hip: groups of 4 to 16 query heads per kv head in one pass,
-larger groups in passes of 16; head sizes 64 and 128; the default for those
-shapes in HBM) against the float64 oracle.
+larger groups in passes of 16; head sizes 32 to 128 in steps of 16; the
+default for those shapes in HBM) against the float64 oracle.
 
 Bars as in test_gpu_decode: fp32 out max-abs <= 2e-3; out in the KV dtype
 fp16 2e-3 / bf16 1.6e-2 (atol and rtol); lse 1e-4 relative; empty rows
@@ -208,3 +208,60 @@ def test_mm_kernel_forced_on_small_groups(gpu, G, D, dtype, monkeypatch):
         for out_dtype in (torch.float32, dtype):
             out, lse = run_host_layout(q, kc, vc, bt, lens, scale, out_dtype, gpu)
             _check(out, lse, ref_out, ref_lse, lens, dtype, gpu)
+
+
+@pytest.mark.parametrize("D", [32, 48, 80, 96, 112])
+@pytest.mark.parametrize("G", [4, 8, 20])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_mm_kernel_head_sizes_between(gpu, D, G, dtype, monkeypatch):
+    """Head sizes that are multiples of 16 but not of 32 (the last q.K step
+    masked past D) or not powers of two (V chunks spread over whole 64-lane
+    loads): host layout and vLLM's, whole rows and forced 2-block splits,
+    fp32 and 16-bit outputs."""
+    KVH = 2
+    H = G * KVH
+    q, kc, vc, bt, lens = _case(H, KVH, D, dtype, seed=G * D + 1)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        for out_dtype in (torch.float32, dtype):
+            out, lse = run_host_layout(q, kc, vc, bt, lens, scale, out_dtype, gpu)
+            _check(out, lse, ref_out, ref_lse, lens, dtype, gpu)
+        o_v = torch.empty(len(LENS), H, D, dtype=torch.float32, device=gpu)
+        o_v, l_v = ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu),
+                                    lens.to(gpu), scale, out=o_v)
+        torch.cuda.synchronize()
+        _check(o_v, l_v, ref_out, ref_lse, lens, dtype, gpu)
+
+
+@pytest.mark.parametrize("D", [80, 96, 112])
+def test_mm_kernel_head_sizes_between_two_tiers(gpu, D):
+    """The fused two-tier launch at those head sizes (both tiers in HBM)."""
+    G, KVH, dtype = 8, 2, torch.bfloat16
+    H = G * KVH
+    lens = [700, 300, 1, 0, 17, 64]
+    n = len(lens)
+    q, kc, vc, bt, ln = _case(H, KVH, D, dtype, seed=D, lens=lens, C=160)
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, ln, scale)
+    W = bt.shape[1]
+    bt0 = torch.zeros(n, W, dtype=torch.int32)
+    bt1 = torch.zeros(n, W, dtype=torch.int32)
+    l0 = torch.zeros(n, dtype=torch.int32)
+    l1 = torch.zeros(n, dtype=torch.int32)
+    for i, L in enumerate(lens):
+        nb = (L + 15) // 16
+        k = nb // 2
+        bt0[i, :k] = bt[i, :k]
+        bt1[i, : nb - k] = bt[i, k:nb]
+        l0[i] = 16 * k
+        l1[i] = L - 16 * k
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    ops.split_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt0.to(gpu), l0.to(gpu), kc.to(gpu),
+                     vc.to(gpu), bt1.to(gpu), l1.to(gpu), scale, out=out, lse=lse)
+    torch.cuda.synchronize()
+    _check(out, lse, ref_out, ref_lse, ln, dtype, gpu)

@@ -97,12 +97,14 @@ struct __align__(16) MmLds {  // 16-byte V rows, float4 merge reads
 
 template <typename T, int D, bool TWO>
 __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledParams p) {
-  static_assert(D == 64 || D == 128, "decode_mm_kernel: head size 64 or 128");
-  constexpr int KS = D / 32;             // scores: 32-dim matrix-core steps
+  static_assert(D % 16 == 0 && D >= 32 && D <= 128, "decode_mm_kernel: D = 16 m, 32..128");
+  constexpr int KS = (D + 31) / 32;      // scores: 32-dim matrix-core steps (the last
+                                         // masked past D when D is not a multiple of 32)
   constexpr int NC = D / 16;             // P.V: 16-dim output chunks
   constexpr int CPT = D / 8;             // V: 16-byte chunks per token row
-  constexpr int TPLD = kWave / CPT;      // V: tokens per load instruction
-  constexpr int NLD = kTileTokens / TPLD;  // V: loads per block
+  constexpr int TC = kTileTokens * CPT;  // V: 16-byte chunks per block
+  constexpr int NLD = (TC + kWave - 1) / kWave;  // V: loads per block (lane l of load j
+                                                 // takes chunk 64 j + l, if < TC)
   constexpr float kPScale = std::is_same<T, F16>::value ? 128.f : 1.f;
 
   __shared__ MmLds<D> lds;
@@ -118,8 +120,9 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
 
   const int col = lane & 15;  // K: token row of the A operand; scores: column
   const int R = lane >> 4;    // K: dims 8R..+7 of each step; scores: tokens 4R..4R+3
-  const int vtok = lane / CPT;   // V: token of load 0 (load j: + TPLD*j)
-  const int vch = lane % CPT;    // V: 16-byte chunk of the token row
+  // K step ks covers dims 8R + 32 ks .. +7 of this lane; past D (the last step
+  // when D is not a multiple of 32) both operands are zero
+  auto k_dims_on = [&](int ks) { return 8 * R + 32 * ks < D; };
 
   // B operand of the scores: column col's head, dims 8R + 32*ks .. +7
   Vec8 qb[KS];
@@ -127,20 +130,31 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
     const uint16_t* qrow =
         p.q + (int64_t)t.i * p.q_ss + (int64_t)task_head(t, col) * p.q_sh + R * 8;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qb[ks] = ld16(qrow + 32 * ks);
+    for (int ks = 0; ks < KS; ++ks)
+      qb[ks] = k_dims_on(ks) ? ld16(qrow + 32 * ks) : Vec8{{0u, 0u, 0u, 0u}};
   }
-  // Byte offsets inside one (block, head) run, per tier: K step ks at
-  // koff + 64*ks; V load j at voff + j*vstep.
+  // V chunk of load j: c = 64 j + lane, token c / CPT, 16-byte slice c % CPT;
+  // row-major in LDS it sits at element 8 c. Byte offsets inside one (block,
+  // head) run, per tier: K step ks at koff + 64*ks, V load j at voff[j].
+  int vtok[NLD];
   const TierParams& t0 = p.tier[0];
   const uint32_t koff0 = (uint32_t)(((int64_t)col * t0.st + R * 8) * 2);
-  const uint32_t voff0 = (uint32_t)(((int64_t)vtok * t0.st + vch * 8) * 2);
-  const uint32_t vstep0 = (uint32_t)((int64_t)TPLD * t0.st * 2);
-  uint32_t koff1 = 0, voff1 = 0, vstep1 = 0;
+  uint32_t voff0[NLD], voff1[NLD], koff1 = 0;
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) {
+    const int c = kWave * j + lane < TC ? kWave * j + lane : 0;  // spare lanes read chunk 0
+    vtok[j] = kWave * j + lane < TC ? c / CPT : kTileTokens;     // and never store it
+    voff0[j] = (uint32_t)(((int64_t)(c / CPT) * t0.st + (c % CPT) * 8) * 2);
+    voff1[j] = 0;
+  }
   if constexpr (TWO) {
     const TierParams& t1 = p.tier[1];
     koff1 = (uint32_t)(((int64_t)col * t1.st + R * 8) * 2);
-    voff1 = (uint32_t)(((int64_t)vtok * t1.st + vch * 8) * 2);
-    vstep1 = (uint32_t)((int64_t)TPLD * t1.st * 2);
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      const int c = kWave * j + lane < TC ? kWave * j + lane : 0;
+      voff1[j] = (uint32_t)(((int64_t)(c / CPT) * t1.st + (c % CPT) * 8) * 2);
+    }
   }
 
   // This wave's V staging, two slots of [16 tokens][D]; the tr16 read of
@@ -169,12 +183,10 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
   auto load_block = [&](int slot, int k) {
     const BlockSrc src = block_src<TWO>(p, wb, t.kh, k);
     const uint32_t koff = src.t1 ? koff1 : koff0;
-    const uint32_t voff = src.t1 ? voff1 : voff0;
-    const uint32_t vstep = src.t1 ? vstep1 : vstep0;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kb[slot][ks] = buffer_ld16(src.k, koff, 64 * ks);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) vb[slot][j] = buffer_ld16(src.v, voff, j * vstep);
+    for (int j = 0; j < NLD; ++j) vb[slot][j] = buffer_ld16(src.v, src.t1 ? voff1[j] : voff0[j]);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -182,7 +194,12 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
   auto block_scores = [&](int slot, int ntok, float* s) {
     f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) sv = mfma_qk<T>(kb[slot][ks], qb[ks], sv);
+    for (int ks = 0; ks < KS; ++ks) {
+      // K past D (the next field of the row, or 0 past the run) times a zero
+      // q could still be NaN: zero it too
+      const Vec8 kv = (32 * (ks + 1) <= D || k_dims_on(ks)) ? kb[slot][ks] : Vec8{{0u, 0u, 0u, 0u}};
+      sv = mfma_qk<T>(kv, qb[ks], sv);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) s[r] = sv[r] * p.scale_log2;
     if (ntok < kTileTokens) {
@@ -197,10 +214,12 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
     uint16_t* st = stage + (k & 1) * kTileTokens * D;
 #pragma unroll
     for (int j = 0; j < NLD; ++j) {
-      Vec8 x = vb[slot][j];
-      if (ntok < kTileTokens && vtok + TPLD * j >= ntok) x = Vec8{{0u, 0u, 0u, 0u}};  // stale V may be NaN
-      *reinterpret_cast<uint4*>(st + (vtok + TPLD * j) * D + vch * 8) =
-          make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
+      if (TC % kWave == 0 || vtok[j] < kTileTokens) {  // a chunk of the block
+        Vec8 x = vb[slot][j];
+        if (ntok < kTileTokens && vtok[j] >= ntok) x = Vec8{{0u, 0u, 0u, 0u}};  // stale V may be NaN
+        *reinterpret_cast<uint4*>(st + 8 * (kWave * j + lane)) =
+            make_uint4(x.w[0], x.w[1], x.w[2], x.w[3]);
+      }
     }
     float bmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     bmax = fmaxf(bmax, shfl_xor_f32(bmax, 16));
@@ -354,7 +373,12 @@ template <typename T>
 hipError_t launch_t(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int D, bool two,
                     hipStream_t s) {
   switch (D) {
+    case 32: return launch_d<T, 32>(tp, tasks, sp, two, s);
+    case 48: return launch_d<T, 48>(tp, tasks, sp, two, s);
     case 64: return launch_d<T, 64>(tp, tasks, sp, two, s);
+    case 80: return launch_d<T, 80>(tp, tasks, sp, two, s);
+    case 96: return launch_d<T, 96>(tp, tasks, sp, two, s);
+    case 112: return launch_d<T, 112>(tp, tasks, sp, two, s);
     case 128: return launch_d<T, 128>(tp, tasks, sp, two, s);
   }
   return hipErrorInvalidValue;

@@ -290,13 +290,25 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   //     chain loses (n = 32: -3 %), and so it does on short rows (L <= 512:
   //     -1 %). G = 2 / 3 and D = 64 stay on the VALU kernel (G = 2, n = 128:
   //     6.79 against 6.74 TB/s; MHA D = 64: 6.50 against 6.03).
-  const bool matrix_ok = matrix && !f32 && D == sp.kernel_d && !kernel_forced("valu");
+  //   * other head sizes: the P.V-on-MFMA kernel is built for every multiple
+  //     of 16 from 32 to 128 (the q.K-only one for 64, 128 and 256 only). At
+  //     D = 32 / 48 / 80 / 96 / 112 (n = 128, L in [256, 2048], bf16) it
+  //     takes groups of 8 at 3.69 / 3.51 / 4.45 / 5.22 / 4.88 TB/s against
+  //     1.80 / 2.63 / 1.99 / 2.39 / 2.78 on the VALU kernel; groups of 4 gain
+  //     where D is a multiple of 32 (D = 32: 3.67 against 3.05; D = 96 ties)
+  //     and tie or lose where the last q.K step is half empty (48 / 80 / 112:
+  //     3.48 / 4.43 / 4.86 against 3.53 / 4.47 / 5.22), so there it takes
+  //     groups of 5 and more. MHA at these sizes loses 5-25 % and stays on the
+  //     VALU kernel. (K + V runs of 320 or 448 bytes straddle cache lines;
+  //     both kernels read those sizes slower.)
+  const bool matrix_ok = matrix && !f32 && !kernel_forced("valu");
   const int cus = device_cus();
   const bool big_mha = G == 1 && D == 128 && cus > 0 && (int64_t)n * KVH >= 8LL * cus &&
                        wt >= 1024 / kTileTokens;
-  sp.mfma = matrix_ok && G >= 4;
-  sp.mm = matrix_ok && D <= 128 &&
-          (kernel_forced("mm") || ((G >= 4 || big_mha) && !kernel_forced("mfma")));
+  const bool mm_g = D % 32 == 0 ? G >= 4 : G >= 5;
+  sp.mfma = matrix_ok && G >= 4 && D == sp.kernel_d;
+  sp.mm = matrix_ok && D % 16 == 0 && D >= 32 && D <= 128 &&
+          (kernel_forced("mm") || ((mm_g || big_mha) && !kernel_forced("mfma")));
   if (sp.mm) {
     sp.mfma = false;
     sp.kernel_g = 16;
