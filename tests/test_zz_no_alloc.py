@@ -41,7 +41,8 @@ def _call(noalloc, q, kc, vc, bt, lens, scale, out, lse, ws=None):
     head = (q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
             kc.stride(0), kc.stride(1), kc.stride(2), C, bt.data_ptr(), bt.stride(0),
             bt.shape[1], lens.data_ptr(), None, n, H, KVH, D, BS, float(scale),
-            _lib.FD_F16 if q.dtype == torch.float16 else _lib.FD_BF16,
+            {torch.float16: _lib.FD_F16, torch.bfloat16: _lib.FD_BF16,
+             torch.float32: _lib.FD_F32}[q.dtype],
             out.data_ptr(), out.stride(0), out.stride(1), _lib.FD_F32,
             lse.data_ptr(), lse.stride(0))
     if noalloc:
@@ -71,7 +72,8 @@ def _case(n, H, KVH, D, dtype, lo, hi, seed, dev):
     return q, kc, vc, bt, lens
 
 
-@pytest.mark.parametrize("H,KVH,dtype", [(32, 8, torch.bfloat16), (32, 32, torch.float16)])
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 8, torch.bfloat16), (32, 32, torch.float16),
+                                         (16, 2, torch.float32)])
 def test_noalloc_matches_workspace_entry_point(gpu, H, KVH, dtype):
     D = 128
     scale = 1.0 / math.sqrt(D)

@@ -1,12 +1,17 @@
-// Grouped-query decode kernel with both products on the matrix cores, for
-// groups of 4 to 16 query heads per kv head (larger groups in passes of 16).
+// Decode kernel with both products on the matrix cores: up to 16 query
+// heads of one kv head per task (larger groups in passes of 16), head sizes
+// 32 to 128 in steps of 16. The planner gives it grouped-query launches and
+// large MHA launches at D = 128 (one real column of 16: the contraction is
+// free next to the read, and its access pattern reads HBM a little faster
+// there than the VALU kernel's).
 //
 // Per 16-token block of one kv head and up to 16 of its query heads (the
 // "columns"; spare columns repeat the task's last head and are never
 // written):
 //   scores  S[16 tokens x 16 columns] = K . Q^T: one v_mfma_f32_16x16x32 per
-//           32 dims, as in decode_mfma.hip; lane l ends with the scores of
-//           tokens 4R..4R+3 (R = l/16) for column l%16;
+//           32 dims (the dims of a last step past D zero in both operands),
+//           as in decode_mfma.hip; lane l ends with the scores of tokens
+//           4R..4R+3 (R = l/16) for column l%16;
 //   softmax per column in the exp2 domain: the block max over the 16 tokens
 //           (an in-lane max of 4, then across the four 16-lane rows), a
 //           running max raised only when a block max passes it by more than
@@ -18,8 +23,9 @@
 //           of p (one part alone keeps 8 for bf16, 11 for fp16); fp16 p is
 //           scaled by 2^7 first (p <= 2^15) so small weights stay normal.
 //           The B operand needs 4 consecutive tokens of one dim per lane:
-//           each wave writes its V block row-major to LDS and reads it back
-//           with ds_read_b64_tr_b16. That instruction (lane mapping checked
+//           each wave writes its V block row-major to LDS (lane l of load j
+//           carries 16-byte chunk 64 j + l of the block, so the loads stay
+//           whole at any D) and reads it back with ds_read_b64_tr_b16. That instruction (lane mapping checked
 //           on the GPU with an in-bounds probe) gives lane 16g+i the element
 //           i%4 of the 64-bit rows addressed by lanes 16g + i/4 + 4k,
 //           k = 0..3; so with lane 16g+j addressing V[token 4g + j/4][dims
