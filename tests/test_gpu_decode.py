@@ -286,10 +286,11 @@ def test_gqa_large_scores_and_range_errors(gpu, kernel, monkeypatch):
                          "on its first run with no cause found by reading; that code path was "
                          "removed, so this test has nothing to run against")
 def test_counters_left_zero_across_calls(gpu, monkeypatch):
-    """The task queue and split-arrival counters are reset by every launch, so
-    calls of different shapes can share one counter array."""
-    from vllm_fastdecoder_amd.ops import WORKSPACE
-
+    """Record of the removed persistent work-queue kernel, whose task queue and
+    split-arrival counters had to be left at zero by every launch so calls of
+    different shapes could share them. The workspace holds no counters now;
+    what remains checkable is that calls of different shapes and task sizes
+    on one workspace agree."""
     w = cases.WORKLOADS["correctness"]
     lens, bt, pool = cases.draw_lens_and_tables(w)
     k, v, _ = cases.kv_pool(w, pool, "host", gpu)
@@ -302,8 +303,6 @@ def test_counters_left_zero_across_calls(gpu, monkeypatch):
             lse = torch.empty(w.H, n, dtype=torch.float32, device=gpu)
             ops.decode_attn(q[:n], k, v, bt[:n].to(gpu), lens[:n].to(gpu), w.scale, out, lse)
             torch.cuda.synchronize()
-            for key, ctr in WORKSPACE._counters.items():
-                assert int(ctr.abs().sum()) == 0, (split, n)
             if n == w.n:
                 if ref is None:
                     ref = out.clone()
