@@ -291,7 +291,9 @@ def test_fused_long_rows(gpu, kernel, H, KVH, dtype, monkeypatch):
 @pytest.mark.parametrize("H,KVH", [(32, 2), (40, 8), (28, 4)])
 def test_fused_any_head_group(gpu, kernel, H, KVH, monkeypatch):
     """Fused two-tier launch with 16 (passes of 8), 5 and 7 (8-slot kernel)
-    query heads per kv head."""
+    query heads per kv head; the host tier lies in pinned memory, so the
+    default is the VALU kernel too (the matrix-core kernels' two-tier form is
+    covered by tests/test_gpu_decode_mm.py with both tiers in HBM)."""
     if kernel == "valu":
         monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
     c = two_tier_case(9, H, KVH, 128, torch.bfloat16, seed=61 + H, dev=gpu)

@@ -41,7 +41,7 @@ constexpr int kWavesPerTask = 4;        // wavefronts sharing one task
 constexpr int kMaxWaveBlocks = kWave;   // a wave's block ids of a task fit one VGPR
 constexpr int kMaxSplitBlocks = kWavesPerTask * kMaxWaveBlocks;
 constexpr int kMaxDevices = 64;         // per-device launch settings cached
-constexpr int kMaxHeadGroup = 512;      // largest H / KVH the tiled kernels take (in passes of 8)
+constexpr int kMaxHeadGroup = 512;      // largest H / KVH the tiled kernels take (in passes)
 constexpr int kMaxBlockSize = 1024;     // largest cache block size they take (16-token tiles)
 
 // One KV tier as the tiled kernels see it (16-bit elements).
