@@ -140,6 +140,36 @@ int fd_paged_decode_workspace_size(
     int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
     int32_t block_size, int32_t bt_width, size_t* bytes);
 
+/* Which kernel a decode launch of these sizes takes, and how it is cut into
+ * tasks (the planner of fd_paged_decode_partial / fd_split_decode, on the
+ * current device). No counterpart in the reference; for tests and for
+ * integrators who want to know what runs.
+ *   kv_dtype    FD_F16 / FD_BF16 / FD_F32
+ *   aligned     1 if the launch meets the tiled kernels' alignment rules
+ *               (16-byte aligned q, out and caches; strides multiples of 8
+ *               elements), else 0 (the generic kernel)
+ *   host_tier   1 if a tier lies in pinned host memory (16-bit launches then
+ *               take the VALU kernel)
+ * FD_DECODE_KERNEL and FD_SPLIT_BLOCKS are honoured as in a launch. */
+#define FD_KERNEL_GENERIC 0 /* any layout, one wave per (sequence, head) */
+#define FD_KERNEL_VALU 1    /* 16-bit KV, vector ALUs */
+#define FD_KERNEL_MFMA 2    /* 16-bit KV, q.K on the matrix cores */
+#define FD_KERNEL_MM 3      /* 16-bit KV, q.K and P.V on the matrix cores */
+#define FD_KERNEL_F32 4     /* fp32 KV */
+
+typedef struct {
+  int32_t kernel;         /* FD_KERNEL_* */
+  int32_t heads_per_task; /* query heads one task takes (its kernel's slots) */
+  int32_t passes;         /* tasks per (sequence, kv head, block range) */
+  int32_t split_blocks;   /* 16-token tiles per task */
+  int32_t max_splits;     /* tasks per row at most (> 1: a combine pass) */
+  int32_t capped;         /* 1: at most two workgroups per compute unit */
+} FdDecodePlan;
+
+int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                        int32_t block_size, int32_t bt_width, int32_t kv_dtype, int32_t aligned,
+                        int32_t host_tier, FdDecodePlan* plan);
+
 /* Size of the device scratch behind fd_paged_decode_partial_noalloc. */
 #define FD_NOALLOC_SCRATCH_BYTES (32u << 20)
 

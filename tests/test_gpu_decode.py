@@ -531,7 +531,8 @@ def test_head_sizes_between_kernels_match_oracle(gpu, D, H, KVH, dtype, monkeypa
 @pytest.mark.parametrize("kernel", ["default", "valu"])
 @pytest.mark.parametrize("H,KVH,D,dtype", [(8, 8, 128, torch.float16), (16, 4, 128, torch.bfloat16),
                                            (12, 2, 96, torch.float16), (32, 4, 128, torch.float16),
-                                           (24, 2, 64, torch.bfloat16)])
+                                           (24, 2, 64, torch.bfloat16), (16, 2, 96, torch.bfloat16),
+                                           (20, 4, 80, torch.float16)])
 def test_larger_cache_blocks_match_oracle(gpu, BS, kernel, H, KVH, D, dtype, monkeypatch):
     """Cache blocks of 16 * m tokens run as m 16-token tiles: host layout and
     vLLM's layout, whole rows and forced 2-tile splits (a split boundary

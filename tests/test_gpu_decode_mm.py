@@ -265,3 +265,24 @@ def test_mm_kernel_head_sizes_between_two_tiers(gpu, D):
                      vc.to(gpu), bt1.to(gpu), l1.to(gpu), scale, out=out, lse=lse)
     torch.cuda.synchronize()
     _check(out, lse, ref_out, ref_lse, ln, dtype, gpu)
+
+
+def test_large_mha_launches_take_the_matrix_core_kernel(gpu, monkeypatch):
+    """MHA at D = 128 takes this kernel once there are >= 8 tasks per CU and
+    rows that may reach 1,024 tokens; smaller launches, short rows, other
+    head sizes and G = 2 stay on the VALU kernel."""
+    monkeypatch.delenv("FD_DECODE_KERNEL", raising=False)
+    monkeypatch.delenv("FD_SPLIT_BLOCKS", raising=False)
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    n_big = 8 * cus // 32  # tasks = n x 32 kv heads = 8 per CU
+
+    def kernel(n, H, KVH, D, W):
+        return ops.decode_plan_info(n, H, KVH, D, 16, W, torch.float16)["kernel"]
+
+    assert kernel(128, 32, 32, 128, 128) == "mm"          # the vicuna-7b shape
+    assert kernel(n_big, 32, 32, 128, 64) == "mm"
+    assert kernel(n_big - 1, 32, 32, 128, 64) == "valu"   # fewer tasks
+    assert kernel(n_big, 32, 32, 128, 63) == "valu"       # rows up to 1,008 tokens
+    assert kernel(128, 32, 32, 96, 128) == "valu"
+    assert kernel(128, 32, 16, 128, 128) == "valu"        # G = 2
+    assert kernel(8, 32, 32, 128, 64) == "valu"           # the small batch

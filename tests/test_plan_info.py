@@ -1,0 +1,95 @@
+"""The planner's kernel choice through fd_decode_plan_info (no GPU needed:
+without a device the CU count is unknown, so the large-MHA rule, which needs
+it, is checked by tests/test_gpu_decode_mm.py)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from vllm_fastdecoder_amd import _lib, ops
+
+F16, BF16, F32 = torch.float16, torch.bfloat16, torch.float32
+
+
+def plan(n, H, KVH, D, W, dtype=BF16, BS=16, **kw):
+    return ops.decode_plan_info(n, H, KVH, D, BS, W, dtype, **kw)
+
+
+@pytest.fixture(autouse=True)
+def _no_overrides(monkeypatch):
+    monkeypatch.delenv("FD_DECODE_KERNEL", raising=False)
+    monkeypatch.delenv("FD_SPLIT_BLOCKS", raising=False)
+
+
+@pytest.mark.parametrize("H,KVH,D,kernel,slots,passes", [
+    (32, 32, 128, "valu", 1, 1),    # MHA (small launch)
+    (32, 16, 128, "valu", 2, 1),    # G = 2
+    (24, 8, 128, "valu", 4, 1),     # G = 3: 4-slot VALU kernel
+    (32, 8, 128, "mm", 16, 1),      # G = 4: both products on the matrix cores
+    (64, 8, 128, "mm", 16, 1),      # G = 8
+    (64, 2, 128, "mm", 16, 2),      # G = 32: two passes of 16
+    (32, 8, 64, "mm", 16, 1),
+    (32, 8, 32, "mm", 16, 1),       # D a multiple of 32: groups of 4
+    (32, 8, 96, "mm", 16, 1),
+    (32, 8, 48, "valu", 4, 1),      # half-empty last q.K step: groups of 4 stay on the VALU
+    (32, 8, 80, "valu", 4, 1),
+    (32, 8, 112, "valu", 4, 1),
+    (40, 8, 112, "mm", 16, 1),      # groups of 5 take it
+    (64, 8, 80, "mm", 16, 1),
+    (32, 8, 256, "mfma", 4, 1),     # D = 256: q.K-only matrix-core kernel
+    (64, 8, 256, "mfma", 8, 1),
+    (32, 8, 72, "valu", 4, 1),      # not a multiple of 16: VALU in its 128 build
+    (32, 8, 160, "valu", 4, 1),
+])
+def test_16bit_kernel_choice(H, KVH, D, kernel, slots, passes):
+    p = plan(128, H, KVH, D, 128)
+    assert (p["kernel"], p["heads_per_task"], p["passes"]) == (kernel, slots, passes), p
+
+
+@pytest.mark.parametrize("H,KVH,D,slots,passes", [
+    (32, 32, 128, 1, 1), (32, 8, 128, 4, 1), (64, 8, 128, 8, 1), (64, 8, 256, 4, 2),
+    (96, 4, 64, 8, 3),
+])
+def test_fp32_takes_its_own_kernel(H, KVH, D, slots, passes):
+    p = plan(64, H, KVH, D, 64, dtype=F32)
+    assert (p["kernel"], p["heads_per_task"], p["passes"]) == ("f32", slots, passes), p
+
+
+def test_host_tier_and_unaligned_launches():
+    # a tier in pinned host memory: 16-bit launches leave the matrix cores
+    assert plan(128, 64, 8, 128, 128, host_tier=True)["kernel"] == "valu"
+    assert plan(128, 64, 8, 128, 128, dtype=F32, host_tier=True)["kernel"] == "f32"
+    # layouts the tiled kernels cannot take
+    assert plan(128, 32, 8, 128, 128, aligned=False)["kernel"] == "generic"
+    assert plan(8, 8, 8, 128, 8, BS=8)["kernel"] == "generic"      # block size not 16 m
+    assert plan(8, 8, 8, 100, 8)["kernel"] == "generic"             # D not a multiple of 8
+    assert plan(8, 8, 8, 512, 8)["kernel"] == "generic"             # D > 256
+    assert plan(8, 8, 8, 128, 8, BS=64)["kernel"] == "valu"         # 4 tiles per block
+
+
+def test_forced_kernels(monkeypatch):
+    monkeypatch.setenv("FD_DECODE_KERNEL", "valu")
+    assert plan(128, 64, 8, 128, 128)["kernel"] == "valu"
+    monkeypatch.setenv("FD_DECODE_KERNEL", "mfma")
+    assert plan(128, 64, 8, 128, 128)["kernel"] == "mfma"
+    assert plan(128, 64, 8, 96, 128)["kernel"] == "valu"            # not built for 96
+    monkeypatch.setenv("FD_DECODE_KERNEL", "mm")
+    assert plan(8, 32, 32, 128, 64)["kernel"] == "mm"
+    assert plan(8, 32, 32, 256, 64)["kernel"] == "valu"             # not built for 256
+
+
+def test_task_split_follows_the_override(monkeypatch):
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", "16")
+    p = plan(4, 32, 8, 128, 100)
+    assert p["split_blocks"] == 16 and p["max_splits"] == 7 and not p["capped"]
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", "64")
+    p = plan(4, 32, 8, 128, 100, BS=32)  # 100 blocks of 32 tokens = 200 tiles
+    assert p["split_blocks"] == 64 and p["max_splits"] == 4 and p["capped"]
+
+
+def test_bad_arguments_raise():
+    with pytest.raises(_lib.FdError):
+        plan(8, 30, 8, 128, 8)           # H not a multiple of KVH
+    with pytest.raises(_lib.FdError):
+        ops.decode_plan_info(8, 32, 8, 128, 16, -1, BF16)

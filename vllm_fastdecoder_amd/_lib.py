@@ -18,8 +18,23 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 6
+ABI_VERSION = 7
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FD_NOALLOC_SCRATCH_BYTES of include/fdattn.h
+
+
+# Kernel families of fd_decode_plan_info (include/fdattn.h).
+FD_KERNEL_NAMES = {0: "generic", 1: "valu", 2: "mfma", 3: "mm", 4: "f32"}
+
+
+class FdDecodePlan(ctypes.Structure):
+    _fields_ = [
+        ("kernel", c_int32),
+        ("heads_per_task", c_int32),
+        ("passes", c_int32),
+        ("split_blocks", c_int32),
+        ("max_splits", c_int32),
+        ("capped", c_int32),
+    ]
 
 
 class FdKvTier(ctypes.Structure):
@@ -63,6 +78,12 @@ SIGNATURES: dict[str, tuple] = {
     "fd_paged_decode_workspace_size": (
         c_int,
         [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, POINTER(c_size_t)],
+    ),
+    "fd_decode_plan_info": (
+        c_int,
+        [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,  # n, H, KVH, D, BS, bt_width
+         c_int32, c_int32, c_int32,                             # kv_dtype, aligned, host_tier
+         POINTER(FdDecodePlan)],
     ),
     "fd_paged_decode_partial_noalloc": (
         c_int,

@@ -157,7 +157,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 6; }
+int fd_abi_version(void) { return 7; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -178,6 +178,35 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
     most = std::max(most, decode_workspace_bytes(sp, n, num_heads, head_size));
   }
   *bytes = most;
+  return FD_OK;
+}
+
+int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                        int32_t block_size, int32_t bt_width, int32_t kv_dtype, int32_t aligned,
+                        int32_t host_tier, FdDecodePlan* plan) {
+  if (plan == nullptr) return set_error(FD_ERR_INVALID, "plan_info: plan is NULL");
+  if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      head_size <= 0 || block_size <= 0 || bt_width < 0)
+    return set_error(FD_ERR_INVALID, "plan_info: bad sizes");
+  if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
+    return set_error(FD_ERR_INVALID, "plan_info: unsupported kv dtype %d", kv_dtype);
+  // the same two-step choice as run_decode: a tier in pinned host memory
+  // re-plans 16-bit launches without the matrix-core kernels
+  SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width, kv_dtype,
+                             aligned != 0);
+  if (host_tier != 0 && (sp.mfma || sp.mm))
+    sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width, kv_dtype,
+                     aligned != 0, false);
+  plan->kernel = !sp.fast ? FD_KERNEL_GENERIC
+                 : kv_dtype == FD_F32 ? FD_KERNEL_F32
+                 : sp.mm ? FD_KERNEL_MM
+                 : sp.mfma ? FD_KERNEL_MFMA
+                           : FD_KERNEL_VALU;
+  plan->heads_per_task = sp.fast ? sp.kernel_g : 1;
+  plan->passes = sp.fast ? sp.passes : 1;
+  plan->split_blocks = sp.split_blocks;
+  plan->max_splits = sp.max_splits;
+  plan->capped = sp.fast && sp.cap_occupancy ? 1 : 0;
   return FD_OK;
 }
 

@@ -120,6 +120,21 @@ def reserve_workspace(stream: torch.cuda.Stream, nbytes: int) -> None:
 _WS_SIZES: dict = {}
 
 
+def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtype: torch.dtype,
+                     aligned: bool = True, host_tier: bool = False) -> dict:
+    """The kernel a decode launch of these sizes takes on the current device and
+    how it is cut into tasks (fd_decode_plan_info): {"kernel": "valu" | "mm" |
+    "mfma" | "f32" | "generic", "heads_per_task", "passes", "split_blocks",
+    "max_splits", "capped"}. Honours FD_DECODE_KERNEL / FD_SPLIT_BLOCKS."""
+    plan = _lib.FdDecodePlan()
+    _lib.check(_lib.load_lib().fd_decode_plan_info(n, H, KVH, D, BS, width, _DT[dtype],
+                                                   int(aligned), int(host_tier),
+                                                   ctypes.byref(plan)))
+    return {"kernel": _lib.FD_KERNEL_NAMES[plan.kernel], "heads_per_task": plan.heads_per_task,
+            "passes": plan.passes, "split_blocks": plan.split_blocks,
+            "max_splits": plan.max_splits, "capped": bool(plan.capped)}
+
+
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
     """Workspace a decode call of this shape needs (remembered per shape and
     task-size override, which the library reads from FD_SPLIT_BLOCKS)."""
