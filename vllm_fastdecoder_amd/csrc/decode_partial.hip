@@ -408,6 +408,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   tp.lse_sh = a.lse_sh;
   tp.S = sp.max_splits;
   tp.split_blocks = sp.split_blocks;
+  tp.xcd_group = a.D % 64 != 0;
   const size_t parts = (size_t)a.n * a.H * sp.max_splits;
   if (sp.max_splits > 1) {
     char* ws = static_cast<char*>(a.workspace);
