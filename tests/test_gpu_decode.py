@@ -611,3 +611,57 @@ def test_launches_on_two_streams_use_their_own_workspace(gpu):
         for got, ref in ((ra, alone[0]), (rb, alone[1])):
             assert torch.equal(got[0], ref[0])
             assert torch.equal(got[1], ref[1])
+
+
+@pytest.mark.parametrize("kernel,H,KVH,D,dtype", [
+    ("valu", 8, 8, 128, torch.float16), ("valu", 16, 2, 64, torch.bfloat16),
+    ("valu", 12, 4, 96, torch.float16), ("mfma", 32, 8, 128, torch.float16),
+    ("mfma", 16, 1, 256, torch.float16), ("mm", 32, 8, 128, torch.float16),
+    ("mm", 40, 8, 96, torch.float16), ("mm", 32, 8, 128, torch.bfloat16),
+    ("generic", 8, 2, 64, torch.float16)])
+def test_16bit_output_is_the_fp32_output_rounded(gpu, kernel, H, KVH, D, dtype, monkeypatch):
+    """A 16-bit output equals the fp32 output of the same call converted to
+    16 bits (round to nearest even), bit for bit, in rows the decode kernel
+    writes directly and in split rows the combine kernel writes: results are
+    rounded to fp32 first, then to 16 bits, as the reference's from_float
+    does (cpu_attn.cpp:76-78), whichever code path writes them."""
+    if kernel in ("valu", "mfma", "mm"):
+        monkeypatch.setenv("FD_DECODE_KERNEL", kernel)
+    BS = 16
+    lens_list = [700, 0, 1, 33, 160, 17, 1500, 64, 257]
+    nbs = [(L + BS - 1) // BS for L in lens_list]
+    C = sum(nbs) + 4
+    n = len(lens_list)
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=max(lens_list),
+                                          seed=D + H + KVH)
+    lens[:] = torch.tensor(lens_list, dtype=torch.int32)
+    perm = torch.randperm(C, generator=torch.Generator().manual_seed(D)).to(torch.int32)
+    bt.zero_()
+    pos = 0
+    for i, nb in enumerate(nbs):  # disjoint blocks
+        bt[i, :nb] = perm[pos: pos + nb]
+        pos += nb
+    scale = 1.0 / math.sqrt(D)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    qd = q.to(gpu)
+    if kernel == "generic":  # a head stride of D + 4 elements takes the generic kernel
+        qp = torch.zeros(n, H, D + 4, dtype=dtype, device=gpu)
+        qp[..., :D] = qd
+        qd = qp[..., :D]
+    kd, vd, btd, lnd = kc.to(gpu), vc.to(gpu), bt.to(gpu), lens.to(gpu)
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        res = {}
+        for odt in (torch.float32, dtype):
+            out = torch.empty(n, H, D, dtype=odt, device=gpu)
+            lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+            ops.decode_attn(qd, kd, vd, btd, lnd, scale, out, lse)
+            res[odt] = (out, lse)
+        torch.cuda.synchronize()
+        o32, l32 = res[torch.float32]
+        o16, l16 = res[dtype]
+        assert torch.equal(o16.view(torch.int16), o32.to(dtype).view(torch.int16))
+        assert torch.equal(l16, l32)
+        assert_out_close(o32, ref_out, 2e-3, mask=nz)
+        assert_lse_close(l32, ref_lse, mask=nz)

@@ -204,10 +204,10 @@ __device__ __forceinline__ void store8(void* out, int64_t off, bool f32, const f
     p[1] = make_float4(o[4], o[5], o[6], o[7]);
   } else if constexpr (!std::is_same<T, F32>::value) {
     uint4 u;
-    u.x = from_f32(T{}, o[0]) | (uint32_t(from_f32(T{}, o[1])) << 16);
-    u.y = from_f32(T{}, o[2]) | (uint32_t(from_f32(T{}, o[3])) << 16);
-    u.z = from_f32(T{}, o[4]) | (uint32_t(from_f32(T{}, o[5])) << 16);
-    u.w = from_f32(T{}, o[6]) | (uint32_t(from_f32(T{}, o[7])) << 16);
+    u.x = to_out(T{}, o[0]) | (uint32_t(to_out(T{}, o[1])) << 16);
+    u.y = to_out(T{}, o[2]) | (uint32_t(to_out(T{}, o[3])) << 16);
+    u.z = to_out(T{}, o[4]) | (uint32_t(to_out(T{}, o[5])) << 16);
+    u.w = to_out(T{}, o[6]) | (uint32_t(to_out(T{}, o[7])) << 16);
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(out) + off) = u;
   }
 }

@@ -75,6 +75,23 @@ __device__ __forceinline__ uint16_t from_f32(BF16, float x) {
   return __builtin_bit_cast(uint16_t, (__bf16)x);
 }
 
+// A result in fp32 -> 16-bit output, rounded twice: to fp32 first (a product
+// computed before the call is an fp32 value), then to nearest even in the
+// 16-bit type, as the reference's from_float does (static_cast<T>(src * mul),
+// fastdecode/csrc/cpu_attn.cpp:76-78). The empty asm keeps the compiler from
+// fusing a preceding multiply into the conversion: a mixed-precision FMA with
+// a 16-bit result rounds the exact product once, which differs in the last
+// bit now and then, and would make outputs depend on which code path wrote
+// them.
+__device__ __forceinline__ uint16_t to_out(F16, float x) {
+  asm("" : "+v"(x));
+  return from_f32(F16{}, x);
+}
+__device__ __forceinline__ uint16_t to_out(BF16, float x) {
+  asm("" : "+v"(x));
+  return from_f32(BF16{}, x);
+}
+
 // Generic scalar load/store by runtime dtype (used by the slow paths).
 __device__ __forceinline__ float load_elem(const void* p, int64_t i, int dt) {
   if (dt == FD_F32) return static_cast<const float*>(p)[i];
@@ -86,9 +103,9 @@ __device__ __forceinline__ void store_elem(void* p, int64_t i, int dt, float x) 
   if (dt == FD_F32) {
     static_cast<float*>(p)[i] = x;
   } else if (dt == FD_F16) {
-    static_cast<uint16_t*>(p)[i] = from_f32(F16{}, x);
+    static_cast<uint16_t*>(p)[i] = to_out(F16{}, x);
   } else {
-    static_cast<uint16_t*>(p)[i] = from_f32(BF16{}, x);
+    static_cast<uint16_t*>(p)[i] = to_out(BF16{}, x);
   }
 }
 

@@ -54,11 +54,11 @@ __device__ __forceinline__ void store4(void* p, int64_t off, int dt, bool vec,
   } else if (vec) {
     uint2 u;
     if (dt == FD_F16) {
-      u.x = from_f32(F16{}, x[0]) | (uint32_t(from_f32(F16{}, x[1])) << 16);
-      u.y = from_f32(F16{}, x[2]) | (uint32_t(from_f32(F16{}, x[3])) << 16);
+      u.x = to_out(F16{}, x[0]) | (uint32_t(to_out(F16{}, x[1])) << 16);
+      u.y = to_out(F16{}, x[2]) | (uint32_t(to_out(F16{}, x[3])) << 16);
     } else {
-      u.x = from_f32(BF16{}, x[0]) | (uint32_t(from_f32(BF16{}, x[1])) << 16);
-      u.y = from_f32(BF16{}, x[2]) | (uint32_t(from_f32(BF16{}, x[3])) << 16);
+      u.x = to_out(BF16{}, x[0]) | (uint32_t(to_out(BF16{}, x[1])) << 16);
+      u.y = to_out(BF16{}, x[2]) | (uint32_t(to_out(BF16{}, x[3])) << 16);
     }
     *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p) + off) = u;
   } else {
