@@ -88,6 +88,22 @@ def test_task_split_follows_the_override(monkeypatch):
     assert p["split_blocks"] == 64 and p["max_splits"] == 4 and p["capped"]
 
 
+def test_task_size_follows_the_block_bytes():
+    """The launch-time model takes a workgroup's stream rate as proportional to
+    a block's K + V bytes below 8 KiB (D = 128 at 16 bits), so at D = 64 the
+    same rows are cut into tasks half as long, and a multi-query launch
+    (71 heads over one kv head, five 16-head passes) splits its rows. Measured
+    (batch 32-128, 1-4k tokens, bf16) these are the best fixed sizes."""
+    assert plan(64, 14, 2, 64, 256)["split_blocks"] == 64
+    assert plan(64, 14, 2, 128, 256)["split_blocks"] == 128
+    assert plan(128, 14, 2, 64, 256)["split_blocks"] == 128
+    assert plan(32, 71, 1, 64, 256)["split_blocks"] == 64
+    # D = 128 at 16 bits, fp32 at D = 64 (8 KiB blocks) and larger blocks: unchanged
+    assert plan(128, 32, 8, 128, 128)["split_blocks"] == 256
+    assert plan(64, 14, 2, 64, 256, dtype=F32)["split_blocks"] == \
+        plan(64, 14, 2, 128, 256)["split_blocks"]
+
+
 def test_bad_arguments_raise():
     with pytest.raises(_lib.FdError):
         plan(8, 30, 8, 128, 8)           # H not a multiple of KVH

@@ -219,16 +219,24 @@ unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache) {
 //   T(sb) = max(longest task bytes / per-workgroup stream rate,
 //               (KV bytes + split partials) / min(HBM rate, tasks * that rate))
 //           + the combine launch when rows split (S > 1).
-// One workgroup streams ~50 GB/s, the GPU ~6 TB/s, and the split costs a
-// second launch of ~8 us: so short, few rows run unsplit (one launch), few
-// long rows split until enough tasks keep HBM busy. The constants were fitted
-// to measured launches of MHA and GQA-4 shapes at D = 128 (batch 1-64,
-// 128-16k tokens), where the choice lands within 4 % of the best split size.
+// One workgroup streams ~50 GB/s when a block of one kv head holds 8 KiB of
+// K and V (D = 128 at 16 bits; its waves keep a block each in flight) and
+// proportionally less for smaller blocks (D = 64: ~25 GB/s), the GPU
+// ~6 TB/s, and the split costs a second launch of ~8 us: so short, few rows
+// run unsplit (one launch), few long rows split until enough tasks keep HBM
+// busy. The constants were fitted to measured launches of MHA and GQA-4
+// shapes at D = 128 (batch 1-64, 128-16k tokens), where the choice lands
+// within 4 % of the best split size; the per-block scaling to a sweep of
+// small-kv-head shapes (8/1, 12/2, 14/2 at D = 64, 28/4, 32/8, 71/1 at D = 64;
+// batch 32-256, 1-4k tokens), where it cut the mean excess over the best
+// fixed size from 7.4 % to 0.7 % (D = 64 rows were split too little).
 int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
                            int32_t bt_width, int32_t elt) {
-  constexpr double kWgRate = 50e9, kHbmRate = 6e12, kCombine = 8e-6, kFill = 0.5;
+  constexpr double kWgRate = 50e9, kWgBlock = 8192.0, kHbmRate = 6e12, kCombine = 8e-6,
+                   kFill = 0.5;
   const int64_t W = bt_width > 0 ? bt_width : 1;
   const double blk = (double)BS * 2.0 * D * elt;  // K and V of one block, one kv head
+  const double wg_rate = kWgRate * std::min(1.0, blk / kWgBlock);
   int32_t best = kMaxSplitBlocks;
   double best_t = 0.0;
   for (int32_t sb = kMaxSplitBlocks; sb >= 16; sb /= 2) {
@@ -238,7 +246,7 @@ int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t
     const double longest = (double)std::min<int64_t>(W, sb) * blk;
     const double kv = (double)n * W * kFill * KVH * blk;
     const double part = split ? (double)n * H * S * kFill * D * 8.0 : 0.0;
-    const double t = std::max(longest / kWgRate, (kv + part) / std::min(kHbmRate, tasks * kWgRate)) +
+    const double t = std::max(longest / wg_rate, (kv + part) / std::min(kHbmRate, tasks * wg_rate)) +
                      (split ? kCombine : 0.0);
     if (sb == kMaxSplitBlocks || t < best_t) {
       best = sb;
