@@ -1,7 +1,8 @@
 """GPU parity of the grouped-query kernel with both products on the matrix
-cores (decode_mm.hip: groups of 4 to 16 query heads per kv head in one pass,
-larger groups in passes of 16; head sizes 32 to 128 in steps of 16; the
-default for those shapes in HBM) against the float64 oracle.
+cores (decode_mm.hip: groups of 4 to 16 query heads per kv head in one pass
+of one 16-column group, larger groups in tasks of two or four column groups
+(four up to D = 64) and passes of those; head sizes 32 to 128 in steps of 16;
+the default for those shapes in HBM) against the float64 oracle.
 
 Bars as in test_gpu_decode: fp32 out max-abs <= 2e-3; out in the KV dtype
 fp16 2e-3 / bf16 1.6e-2 (atol and rtol); lse 1e-4 relative; empty rows
@@ -61,13 +62,16 @@ def _check(out, lse, ref_out, ref_lse, lens, dtype, gpu):
     assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
 
 
-@pytest.mark.parametrize("G", [4, 5, 8, 12, 16, 20])
+@pytest.mark.parametrize("G", [4, 5, 8, 12, 16, 20, 32, 36, 48, 71])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_mm_kernel_matches_oracle(gpu, G, D, dtype, monkeypatch):
     """Host layout and vLLM's layout; whole rows, forced 2-block splits
     (split partials of 16 columns, the combine kernel) and the model's own
-    choice; fp32 and 16-bit outputs."""
+    choice; fp32 and 16-bit outputs. Groups past 16 heads take two or four
+    column groups per task (20, 32: two; 36, 48, 71 at D = 64: four, with 28 /
+    16 / 57 spare columns in the last pass; 36, 48, 71 at D = 128: passes of
+    two)."""
     KVH = 2
     H = G * KVH
     q, kc, vc, bt, lens = _case(H, KVH, D, dtype, seed=G * D)
@@ -92,8 +96,14 @@ def test_mm_kernel_extreme_scores(gpu, dtype, kind):
     """Scores far from N(0,1): q x 300 (logits in the hundreds); q x 12 over
     2,000-token rows, so nearly every weight is tiny next to the largest
     (the case where a single 16-bit p would lose the most); K rows scaled up
-    along the row, so the running max is raised again and again."""
-    G, KVH, D = 8, 2, 128
+    along the row, so the running max is raised again and again. Groups of 8
+    at D = 128 and of 40 at D = 64 (four column groups per task, each with its
+    own running max)."""
+    for G, KVH, D in ((8, 2, 128), (40, 1, 64)):
+        _extreme_case(gpu, dtype, kind, G, KVH, D)
+
+
+def _extreme_case(gpu, dtype, kind, G, KVH, D):
     H = G * KVH
     lens = [2000, 1500, 17, 0, 1, 640]
     q, kc, vc, bt, ln = _case(H, KVH, D, torch.float32, seed=77, lens=lens, C=320)
@@ -114,8 +124,9 @@ def test_mm_kernel_extreme_scores(gpu, dtype, kind):
     _check(out, lse, ref_out, ref_lse, ln, dtype, gpu)
 
 
-def test_mm_kernel_range_errors_poison_only_their_rows(gpu):
-    G, KVH, D = 16, 2, 128
+@pytest.mark.parametrize("G,D", [(16, 128), (48, 64)])
+def test_mm_kernel_range_errors_poison_only_their_rows(gpu, G, D):
+    KVH = 2
     H = G * KVH
     q, kc, vc, bt, lens = _case(H, KVH, D, torch.bfloat16, seed=5)
     lens[:4] = torch.tensor([64, 40, 33, 17], dtype=torch.int32)
@@ -136,7 +147,7 @@ def test_mm_kernel_range_errors_poison_only_their_rows(gpu):
     assert_lse_close(lse, ref_lse, mask=ok)
 
 
-@pytest.mark.parametrize("G", [8, 16])
+@pytest.mark.parametrize("G", [8, 16, 48])
 def test_mm_kernel_two_tiers_in_hbm(gpu, G):
     """The fused two-tier launch on this kernel: both tiers in HBM (a tier in
     pinned host memory takes the VALU kernel), each row's blocks split
@@ -211,7 +222,7 @@ def test_mm_kernel_forced_on_small_groups(gpu, G, D, dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("D", [32, 48, 80, 96, 112])
-@pytest.mark.parametrize("G", [4, 8, 20])
+@pytest.mark.parametrize("G", [4, 8, 20, 40])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_mm_kernel_head_sizes_between(gpu, D, G, dtype, monkeypatch):
     """Head sizes that are multiples of 16 but not of 32 (the last q.K step

@@ -319,7 +319,11 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
           (kernel_forced("mm") || ((mm_g || big_mha) && !kernel_forced("mfma")));
   if (sp.mm) {
     sp.mfma = false;
-    sp.kernel_g = 16;
+    // more than 16 heads per kv head (multi-query models): tasks of two or
+    // four groups of 16 columns (four up to D = 64, where the registers
+    // allow), so fewer passes re-read the blocks
+    const int cg = G <= 16 ? 1 : (G <= 32 || D > 64) ? 2 : 4;
+    sp.kernel_g = 16 * cg;
   }
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
   int sb = split_blocks_override();

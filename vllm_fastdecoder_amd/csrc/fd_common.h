@@ -208,7 +208,7 @@ struct SplitPlan {
   bool mfma;             // grouped-query scores on the matrix cores (G >= 4 at D = 256)
   bool mm;               // scores and P.V on the matrix cores (G >= 4, D <= 128)
   bool cap_occupancy;    // long tasks: at most two workgroups per CU
-  int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4, 8 or 16
+  int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4, 8, 16, 32 or 64
   int32_t kernel_d;      // head size the tiled kernel is built for: 64, 128 or 256
   int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
                          // kernel_g), each over the same blocks
