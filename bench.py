@@ -130,7 +130,7 @@ def cpu_baseline(w, lens, bt, pool, q_cpu, iters):
     import torch
 
     import oracle
-    from tests import cases
+    from vllm_fastdecoder_amd import workloads as cases
 
     cores = len(os.sched_getaffinity(0))
     k, v, _ = cases.kv_pool(w, pool, "host", "cuda")
@@ -248,7 +248,7 @@ def hybrid_profile(w, lens, bt, q, frac, steps, warmup, stream):
     of the GPU side): per-step time and the host cores' time."""
     import torch
 
-    from tests import cases
+    from vllm_fastdecoder_amd import workloads as cases
     from vllm_fastdecoder_amd import ops
 
     t = cases.split_tiers(w, lens, bt, q.device)
@@ -275,7 +275,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     (ops.split_decode), the host cores alone, and the hybrid split."""
     import torch
 
-    from tests import cases
+    from vllm_fastdecoder_amd import workloads as cases
     from vllm_fastdecoder_amd import ops
 
     dev = q.device
@@ -419,7 +419,7 @@ class DecodeLeg:
     def __init__(self, w, layout, dev, copies=1):
         import torch
 
-        from tests import cases
+        from vllm_fastdecoder_amd import workloads as cases
         from vllm_fastdecoder_amd import ops
 
         self.w, self.layout, self.dev, self.copies = w, layout, dev, copies
@@ -547,7 +547,7 @@ def main() -> int:
         return 2
     import torch
 
-    from tests import cases
+    from vllm_fastdecoder_amd import workloads as cases
     from vllm_fastdecoder_amd import ops
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
