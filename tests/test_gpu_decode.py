@@ -665,3 +665,42 @@ def test_16bit_output_is_the_fp32_output_rounded(gpu, kernel, H, KVH, D, dtype, 
         assert torch.equal(l16, l32)
         assert_out_close(o32, ref_out, 2e-3, mask=nz)
         assert_lse_close(l32, ref_lse, mask=nz)
+
+
+@pytest.mark.parametrize("H,KVH,D,BS,kernel", [
+    (512, 1, 64, 16, "mm"),        # the largest group the tiled kernels take: 8 passes of 64
+    (513, 1, 64, 16, "generic"),   # one past it
+    (8, 2, 128, 1024, "mm"),       # the largest cache block: 64 tiles per block
+    (8, 2, 128, 2048, "generic"),  # one size past it
+])
+def test_limits_of_the_tiled_kernels(gpu, H, KVH, D, BS, kernel, monkeypatch):
+    """At the tiled kernels' limits (512 query heads per kv head, cache blocks
+    of 1,024 tokens) and one step past them (the generic kernel): the planner's
+    choice, and parity with the oracle on rows of 0, 1, partial and several
+    blocks, whole rows and the model's split."""
+    dtype = torch.bfloat16
+    lens_list = [3 * BS + 5, 0, 1, BS, 2 * BS - 1, 700]
+    n = len(lens_list)
+    nbs = [(L + BS - 1) // BS for L in lens_list]
+    C = sum(nbs) + 2
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=max(lens_list),
+                                          seed=H + BS)
+    lens[:] = torch.tensor(lens_list, dtype=torch.int32)
+    perm = torch.randperm(C, generator=torch.Generator().manual_seed(BS)).to(torch.int32)
+    bt.zero_()
+    pos = 0
+    for i, nb in enumerate(nbs):
+        bt[i, :nb] = perm[pos: pos + nb]
+        pos += nb
+    scale = 1.0 / math.sqrt(D)
+    info = ops.decode_plan_info(n, H, KVH, D, BS, bt.shape[1], dtype)
+    assert info["kernel"] == kernel, info
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    for split in ("0", "2"):
+        monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+        out, lse = run_host_layout(q, kc, vc, bt, lens, scale, torch.float32, gpu)
+        assert_out_close(out, ref_out, 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0)
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
