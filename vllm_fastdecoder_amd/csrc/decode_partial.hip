@@ -12,7 +12,15 @@ namespace {
 // Combines the split partials of every (sequence, head) whose row used more
 // than one task: the N-way form of the log-sum-exp merge. One thread per 4
 // output elements; each thread reads the row's split LSEs (L1-shared with its
-// neighbours) and its slice of every split's partial.
+// neighbours) and its slice of every split's partial. The reads go out
+// kSplitChunk splits at a time, all in flight together, and the first
+// chunk's with the row lengths' (the workspace holds S splits per pair, so
+// they are in bounds before the row's split count is known): a launch of a
+// few rows is a chain of dependent memory round trips, and a loop issuing
+// one split's read per iteration made it one per split. Batched, split
+// launches of 1-8 rows take 0.6-0.8 us less. Splits are summed in index order.
+constexpr int kSplitChunk = 8;
+
 __global__ __launch_bounds__(256) void combine_splits_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ lens_a, const int32_t* __restrict__ lens_b, int32_t width_a,
@@ -26,6 +34,15 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(
   const int64_t pair = tid / per_row;
   const int i = (int)(pair / H);
   const int h = (int)(pair % H);
+  const float* pl = part_lse + pair * S;
+  const float4* po = reinterpret_cast<const float4*>(part_o + pair * S * D) + c;
+  float l0[kSplitChunk];
+  float4 o0[kSplitChunk];
+#pragma unroll
+  for (int u = 0; u < kSplitChunk; ++u) {
+    l0[u] = u < S ? pl[u] : neg_inf();
+    o0[u] = u < S ? po[(int64_t)u * per_row] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
   const int La = lens_a[i];
   const int Lb = lens_b != nullptr ? lens_b[i] : 0;
   if (La > width_a * block_size || Lb > width_b * block_size) return;  // range error: NaN
@@ -33,22 +50,40 @@ __global__ __launch_bounds__(256) void combine_splits_kernel(
                  (Lb > 0 ? (Lb + block_size - 1) / block_size : 0);
   const int ns = (nb + split_blocks - 1) / split_blocks;
   if (ns <= 1) return;  // written directly by the partial kernel
-  const float* pl = part_lse + pair * S;
   float M = neg_inf();
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pl[s]);
+  for (int s0 = 0; s0 < ns; s0 += kSplitChunk) {
+    float v[kSplitChunk];
+#pragma unroll
+    for (int u = 0; u < kSplitChunk; ++u)
+      v[u] = s0 == 0 ? l0[u] : (s0 + u < ns ? pl[s0 + u] : neg_inf());
+#pragma unroll
+    for (int u = 0; u < kSplitChunk; ++u)
+      if (s0 + u < ns) M = fmaxf(M, v[u]);
+  }
   const float Ms = M == neg_inf() ? 0.f : M;
   float wsum = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  const float4* po = reinterpret_cast<const float4*>(part_o + pair * S * D) + c;
-#pragma unroll 4
-  for (int s = 0; s < ns; ++s) {
-    const float w = __expf(pl[s] - Ms);
-    const float4 x = po[(int64_t)s * (D / 4)];
-    wsum += w;
-    acc.x += w * x.x;
-    acc.y += w * x.y;
-    acc.z += w * x.z;
-    acc.w += w * x.w;
+  for (int s0 = 0; s0 < ns; s0 += kSplitChunk) {
+    float lv[kSplitChunk];
+    float4 ov[kSplitChunk];
+#pragma unroll
+    for (int u = 0; u < kSplitChunk; ++u) {
+      const bool on = s0 + u < ns;
+      lv[u] = s0 == 0 ? l0[u] : (on ? pl[s0 + u] : neg_inf());
+      ov[u] = s0 == 0 ? o0[u] : (on ? po[(int64_t)(s0 + u) * per_row] : make_float4(0.f, 0.f, 0.f, 0.f));
+    }
+#pragma unroll
+    for (int u = 0; u < kSplitChunk; ++u) {
+      if (s0 + u < ns) {
+        const float w = __expf(lv[u] - Ms);
+        const float4 x = ov[u];
+        wsum += w;
+        acc.x += w * x.x;
+        acc.y += w * x.y;
+        acc.z += w * x.z;
+        acc.w += w * x.w;
+      }
+    }
   }
   const float inv = 1.f / wsum;
   const int64_t ob = (int64_t)i * out_ss + (int64_t)h * out_sh + c * 4;
