@@ -247,10 +247,12 @@ def test_mm_kernel_head_sizes_between(gpu, D, G, dtype, monkeypatch):
         _check(o_v, l_v, ref_out, ref_lse, lens, dtype, gpu)
 
 
-@pytest.mark.parametrize("D", [80, 96, 112])
-def test_mm_kernel_head_sizes_between_two_tiers(gpu, D):
-    """The fused two-tier launch at those head sizes (both tiers in HBM)."""
-    G, KVH, dtype = 8, 2, torch.bfloat16
+@pytest.mark.parametrize("D,G", [(80, 8), (96, 8), (112, 8), (96, 36), (48, 40), (64, 71)])
+def test_mm_kernel_head_sizes_between_two_tiers(gpu, D, G):
+    """The fused two-tier launch at those head sizes (both tiers in HBM), and
+    with two or four column groups per task (36 at D = 96: passes of 32; 40 at
+    D = 48 and 71 at D = 64: tasks of 64)."""
+    KVH, dtype = 2, torch.bfloat16
     H = G * KVH
     lens = [700, 300, 1, 0, 17, 64]
     n = len(lens)
