@@ -1,0 +1,95 @@
+"""Seeded random shapes across the planner's whole dispatch table against the
+float64 oracle: head counts (MHA, GQA with groups of 2-71 heads, one kv
+head), head sizes (multiples of 8 up to 256, including the sizes the tiled
+kernels build and the ones they run in a larger build), cache blocks of 16-64
+tokens, fp16 / bf16 / fp32, forced task sizes from 1 block to whole rows,
+16-bit and fp32 outputs, both cache layouts. Each case states the kernel the
+planner chose, so a failure names the dispatch path. Same bars as
+test_gpu_decode and test_gpu_decode_f32: fp32 out 2e-3 for 16-bit KV and
+5e-5 for fp32 KV; 16-bit out at the reference's tolerances; lse 1e-4
+relative; empty rows exactly 0 / -inf.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import cases
+from tests.test_gpu_decode import OUT_TOL_16BIT, assert_lse_close, assert_out_close
+from vllm_fastdecoder_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+N_CASES = 64
+HEADS = [(8, 8), (32, 32), (16, 8), (12, 4), (24, 8), (32, 8), (40, 8), (28, 4), (64, 8),
+         (32, 2), (48, 2), (40, 1), (71, 1), (16, 1), (96, 2)]
+HEAD_SIZES = [32, 48, 64, 72, 80, 96, 112, 128, 160, 192, 256]
+BLOCK_SIZES = [16, 16, 16, 32, 64]
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+SPLITS = ["0", "0", "1", "3", "16"]
+
+
+def _draw(i):
+    r = np.random.default_rng(1000 + i)
+    H, KVH = HEADS[r.integers(len(HEADS))]
+    D = int(HEAD_SIZES[r.integers(len(HEAD_SIZES))])
+    BS = int(BLOCK_SIZES[r.integers(len(BLOCK_SIZES))])
+    dtype = DTYPES[r.integers(len(DTYPES))]
+    n = int(r.integers(1, 7))
+    lens = [int(x) for x in r.integers(0, 700, n)]
+    lens[0] = int(r.integers(1, 1200))
+    split = SPLITS[r.integers(len(SPLITS))]
+    out16 = bool(r.integers(2)) and dtype != torch.float32
+    layout = "vllm" if r.integers(2) else "host"
+    return H, KVH, D, BS, dtype, lens, split, out16, layout
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_shape_matches_oracle(gpu, i, monkeypatch):
+    H, KVH, D, BS, dtype, lens_l, split, out16, layout = _draw(i)
+    n = len(lens_l)
+    nbs = [(L + BS - 1) // BS for L in lens_l]
+    C = sum(nbs) + 2
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=max(lens_l),
+                                          seed=i)
+    lens[:] = torch.tensor(lens_l, dtype=torch.int32)
+    perm = torch.randperm(C, generator=torch.Generator().manual_seed(i)).to(torch.int32)
+    bt.zero_()
+    pos = 0
+    for r, nb in enumerate(nbs):
+        bt[r, :nb] = perm[pos: pos + nb]
+        pos += nb
+    scale = 1.0 / math.sqrt(D)
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+    info = ops.decode_plan_info(n, H, KVH, D, BS, bt.shape[1], dtype)
+    what = (f"case {i}: H={H} KVH={KVH} D={D} BS={BS} {dtype} lens={lens_l} split={split} "
+            f"out16={out16} layout={layout} plan={info}")
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    out_dtype = dtype if out16 else torch.float32
+    out = torch.empty(n, H, D, dtype=out_dtype, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    if layout == "host":
+        ops.decode_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), bt.to(gpu), lens.to(gpu), scale, out,
+                        lse)
+    else:
+        kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+        ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu), lens.to(gpu), scale,
+                         out=out, lse=lse)
+    torch.cuda.synchronize()
+    nz = lens > 0
+    try:
+        if out16:
+            tol = OUT_TOL_16BIT[dtype]
+            assert_out_close(out, ref_out, tol, tol, mask=nz)
+        else:
+            assert_out_close(out, ref_out, 5e-5 if dtype == torch.float32 else 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0), "empty rows: out not 0"
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)])), "empty rows: lse not -inf"
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None
