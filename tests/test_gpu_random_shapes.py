@@ -93,3 +93,70 @@ def test_random_shape_matches_oracle(gpu, i, monkeypatch):
         assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)])), "empty rows: lse not -inf"
     except AssertionError as e:
         raise AssertionError(f"{what}: {e}") from None
+
+
+@pytest.mark.parametrize("i", range(32))
+def test_random_two_tier_split_matches_oracle(gpu, i, monkeypatch):
+    """The fused two-tier launch on random shapes: each row's first k blocks
+    (k drawn from 0 to all of them) in an HBM tier in vLLM's layout, the rest in
+    a host-layout tier, in HBM or (every third case) in pinned host memory read
+    zero-copy, against the oracle over the row's blocks as one list."""
+    from vllm_fastdecoder_amd.pinned import pinned_empty
+
+    H, KVH, D, BS, dtype, lens_l, split, out16, _ = _draw(500 + i)
+    r = np.random.default_rng(2000 + i)
+    n = len(lens_l)
+    nbs = [(L + BS - 1) // BS for L in lens_l]
+    C = sum(nbs) + 2
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=max(lens_l),
+                                          seed=500 + i)
+    lens[:] = torch.tensor(lens_l, dtype=torch.int32)
+    perm = torch.randperm(C, generator=torch.Generator().manual_seed(500 + i)).to(torch.int32)
+    bt.zero_()
+    pos = 0
+    for row, nb in enumerate(nbs):
+        bt[row, :nb] = perm[pos: pos + nb]
+        pos += nb
+    W = bt.shape[1]
+    bt0 = torch.zeros(n, W, dtype=torch.int32)
+    bt1 = torch.zeros(n, W, dtype=torch.int32)
+    l0 = torch.zeros(n, dtype=torch.int32)
+    l1 = torch.zeros(n, dtype=torch.int32)
+    for row, (L, nb) in enumerate(zip(lens_l, nbs)):
+        k = int(r.integers(0, nb + 1))
+        bt0[row, :k] = bt[row, :k]
+        bt1[row, : nb - k] = bt[row, k:nb]
+        l0[row] = L if k == nb else k * BS
+        l1[row] = L - int(l0[row])
+    pinned = i % 3 == 0
+    scale = 1.0 / math.sqrt(D)
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", split)
+    what = (f"case {i}: H={H} KVH={KVH} D={D} BS={BS} {dtype} lens={lens_l} split={split} "
+            f"out16={out16} pinned={pinned} l0={l0.tolist()}")
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    if pinned:
+        hk = pinned_empty(kc.shape, kc.dtype)
+        hv = pinned_empty(vc.shape, vc.dtype)
+        hk.copy_(kc)
+        hv.copy_(vc)
+    else:
+        hk, hv = kc.to(gpu), vc.to(gpu)
+    out_dtype = dtype if out16 else torch.float32
+    out = torch.empty(n, H, D, dtype=out_dtype, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    ops.split_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt0.to(gpu), l0.to(gpu), hk, hv,
+                     bt1.to(gpu), l1.to(gpu), scale, out=out, lse=lse)
+    torch.cuda.synchronize()
+    nz = lens > 0
+    try:
+        if out16:
+            tol = OUT_TOL_16BIT[dtype]
+            assert_out_close(out, ref_out, tol, tol, mask=nz)
+        else:
+            assert_out_close(out, ref_out, 5e-5 if dtype == torch.float32 else 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0), "empty rows: out not 0"
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)])), "empty rows: lse not -inf"
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None
