@@ -28,8 +28,9 @@
 //           The B operand needs 4 consecutive tokens of one dim per lane:
 //           each wave writes its V block row-major to LDS (lane l of load j
 //           carries 16-byte chunk 64 j + l of the block, so the loads stay
-//           whole at any D) and reads it back with ds_read_b64_tr_b16. That instruction (lane mapping checked
-//           on the GPU with an in-bounds probe) gives lane 16g+i the element
+//           whole at any D) and reads it back with ds_read_b64_tr_b16.
+//           That instruction (lane mapping checked on the GPU with an
+//           in-bounds probe) gives lane 16g+i the element
 //           i%4 of the 64-bit rows addressed by lanes 16g + i/4 + 4k,
 //           k = 0..3; so with lane 16g+j addressing V[token 4g + j/4][dims
 //           16c + 4(j%4) ..+3], lane 16g+i receives V[tokens 4g..4g+3][dim
@@ -117,6 +118,13 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
   constexpr int NLD = (TC + kWave - 1) / kWave;  // V: loads per block (lane l of load j
                                                  // takes chunk 64 j + l, if < TC)
   constexpr float kPScale = std::is_same<T, F16>::value ? 128.f : 1.f;
+  // K is read in 64-byte column slices, so most lines are read by two loads
+  // of the wave; below 128 dims (64 aside) non-temporal lines were often
+  // fetched twice. Measured (n = 128, 40/8 heads, bf16, L in [1024, 4096]):
+  // the default policy reads D = 32 / 48 / 80 / 96 / 112 at 4.6 / 5.5 / 5.8 /
+  // 5.8 / 5.9 TB/s against 3.9 / 3.7 / 4.7 / 5.5 / 5.2 non-temporal, and
+  // D = 64 / 128 at 5.6 / 6.0 against 6.1 / 6.2.
+  constexpr int POL = (D == 64 || D == 128) ? kKvLoadPolicy : kKvLoadKeep;
 
   __shared__ MmLds<D> lds;
 
@@ -202,9 +210,10 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
     const BlockSrc src = block_src<TWO>(p, wb, t.kh, k);
     const uint32_t koff = src.t1 ? koff1 : koff0;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) kb[slot][ks] = buffer_ld16(src.k, koff, 64 * ks);
+    for (int ks = 0; ks < KS; ++ks) kb[slot][ks] = buffer_ld16<POL>(src.k, koff, 64 * ks);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) vb[slot][j] = buffer_ld16(src.v, src.t1 ? voff1[j] : voff0[j]);
+    for (int j = 0; j < NLD; ++j)
+      vb[slot][j] = buffer_ld16<POL>(src.v, src.t1 ? voff1[j] : voff0[j]);
     __builtin_amdgcn_sched_barrier(0);
   };
 

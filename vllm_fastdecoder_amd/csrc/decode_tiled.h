@@ -136,11 +136,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const uint16_t* base
 // hint keeps the stream from displacing other lines). Measured +7.6 % at the
 // vicuna-7b shape over the default policy.
 constexpr int kKvLoadPolicy = 2;
+// The default policy, for loads whose cache lines are read again soon by
+// another load: a line split between two loads of one wave (the matrix-core
+// kernel's K column slices at head sizes other than 64 and 128) or between
+// the runs of neighbouring heads (K + V runs of 4D bytes that are not whole
+// lines in vLLM's layout, e.g. D = 80). There, non-temporal lines are often
+// gone before their second reader comes and are fetched twice.
+constexpr int kKvLoadKeep = 0;
 
 // 16 bytes at byte `off` (per lane) + `soff` (wave-uniform) of the resource.
+template <int POL = kKvLoadPolicy>
 __device__ __forceinline__ Vec8 buffer_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off,
                                             uint32_t soff = 0) {
-  const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, kKvLoadPolicy);
+  const auto u = __builtin_amdgcn_raw_buffer_load_b128(r, off, soff, POL);
   return Vec8{{(uint32_t)u[0], (uint32_t)u[1], (uint32_t)u[2], (uint32_t)u[3]}};
 }
 

@@ -22,7 +22,7 @@ namespace {
 // tier 0 keeps V right after K in each token row (vLLM's [B, BS, KVH, 2D]
 // cache; D = 128 or 256), and each load reads whole K + V runs of its tokens
 // (512 B at D = 128) instead of K and V rows in separate loads.
-template <typename T, int D, int G, bool TWO, bool ADJ>
+template <typename T, int D, int G, bool TWO, bool ADJ, bool KEEP>
 __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(TiledParams p) {
   constexpr int LPT = D / 8;                // lanes per token row
   constexpr int TPW = kWave / LPT;          // token rows per load instruction
@@ -111,10 +111,11 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
     } else {
       const uint32_t off = src.t1 ? off1 : off0;
       const uint32_t step = src.t1 ? step1 : step0;
+      constexpr int POL = KEEP ? kKvLoadKeep : kKvLoadPolicy;
 #pragma unroll
-      for (int j = 0; j < STEPS; ++j) kb[slot][j] = buffer_ld16(src.k, off, j * step);
+      for (int j = 0; j < STEPS; ++j) kb[slot][j] = buffer_ld16<POL>(src.k, off, j * step);
 #pragma unroll
-      for (int j = 0; j < STEPS; ++j) vb[slot][j] = buffer_ld16(src.v, off, j * step);
+      for (int j = 0; j < STEPS; ++j) vb[slot][j] = buffer_ld16<POL>(src.v, off, j * step);
     }
     // keep the prefetch at the top of the reduction that overlaps it
     __builtin_amdgcn_sched_barrier(0);
@@ -200,16 +201,29 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   finish_task<T, D, G>(p, t, ws, lane);
 }
 
+template <typename T, int D, int G, bool ADJ, bool KEEP>
+hipError_t launch_mode(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
+                       hipStream_t s) {
+  return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, ADJ, KEEP>>(tp, tasks, sp, s)
+             : launch_capped<&decode_tiled_kernel<T, D, G, false, ADJ, KEEP>>(tp, tasks, sp, s);
+}
+
 template <typename T, int D, int G>
 hipError_t launch_dg(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
                      hipStream_t s) {
   if constexpr (D == 128 || D == 256) {
-    if (tp.tier[0].kv_adj)
-      return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, true>>(tp, tasks, sp, s)
-                 : launch_capped<&decode_tiled_kernel<T, D, G, false, true>>(tp, tasks, sp, s);
+    if (tp.tier[0].kv_adj) return launch_mode<T, D, G, true, false>(tp, tasks, sp, two, s);
   }
-  return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, false>>(tp, tasks, sp, s)
-             : launch_capped<&decode_tiled_kernel<T, D, G, false, false>>(tp, tasks, sp, s);
+  if constexpr (D == 128) {
+    // head sizes run in the 128 build whose heads' K + V runs (4 D bytes in
+    // vLLM's layout) are not whole lines: neighbouring heads share lines,
+    // and the default policy keeps them for the second reader. Measured
+    // (n = 128, MHA, bf16, L in [1024, 4096]): D = 72 / 80 / 112 at 5.56 /
+    // 5.79 / 5.64 TB/s against 4.66 / 5.00 / 5.56 non-temporal; D = 96
+    // (whole lines) 5.88 against 6.02, so it stays non-temporal.
+    if (tp.D % 32 != 0) return launch_mode<T, D, G, false, true>(tp, tasks, sp, two, s);
+  }
+  return launch_mode<T, D, G, false, false>(tp, tasks, sp, two, s);
 }
 
 template <typename T, int D>
