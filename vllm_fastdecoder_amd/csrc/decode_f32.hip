@@ -21,7 +21,7 @@ namespace fd {
 
 namespace {
 
-template <int D, int G, bool TWO>
+template <int D, int G, bool TWO, bool KEEP>
 __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(TiledParams p) {
   constexpr int LPT = D / 8;                // lanes per token row (8 values each)
   constexpr int TPW = kWave / LPT;          // token rows per pair of loads
@@ -87,6 +87,11 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(Tiled
   const WaveBlocks wb = wave_blocks<TWO>(p, t, wave, lane);
   const int nu = 2 * wb.nw;  // half blocks of this wave: u = 2k + (second half)
 
+  // head sizes below 128 run in the 128 build read with the default cache
+  // policy (kKvLoadKeep). Measured (n = 128, MHA, L in [256, 2048]):
+  // D = 72 / 80 / 96 / 112 at 5.95 / 5.91 / 5.87 / 5.84 TB/s against
+  // 4.17 / 4.27 / 5.47 / 4.65 non-temporal; D = 128 reads 6.25 either way.
+  constexpr int POL = KEEP ? kKvLoadKeep : kKvLoadPolicy;
   Vec8 kb[2][STEPS][2], vb[2][STEPS][2];
   auto load_half = [&](int slot, int u) {
     const BlockSrc src = block_src<TWO>(p, wb, t.kh, u >> 1);
@@ -95,13 +100,13 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(Tiled
     const uint32_t base = (u & 1) ? (src.t1 ? half1 : half0) : 0u;
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
-      kb[slot][j][0] = buffer_ld16(src.k, off, base + j * step);
-      kb[slot][j][1] = buffer_ld16(src.k, off + 16, base + j * step);
+      kb[slot][j][0] = buffer_ld16<POL>(src.k, off, base + j * step);
+      kb[slot][j][1] = buffer_ld16<POL>(src.k, off + 16, base + j * step);
     }
 #pragma unroll
     for (int j = 0; j < STEPS; ++j) {
-      vb[slot][j][0] = buffer_ld16(src.v, off, base + j * step);
-      vb[slot][j][1] = buffer_ld16(src.v, off + 16, base + j * step);
+      vb[slot][j][0] = buffer_ld16<POL>(src.v, off, base + j * step);
+      vb[slot][j][1] = buffer_ld16<POL>(src.v, off + 16, base + j * step);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
@@ -189,8 +194,13 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(Tiled
 template <int D, int G>
 hipError_t launch_dg(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
                      hipStream_t s) {
-  return two ? launch_capped<&decode_f32_kernel<D, G, true>>(tp, tasks, sp, s)
-             : launch_capped<&decode_f32_kernel<D, G, false>>(tp, tasks, sp, s);
+  if constexpr (D == 128) {
+    if (tp.D != 128)
+      return two ? launch_capped<&decode_f32_kernel<D, G, true, true>>(tp, tasks, sp, s)
+                 : launch_capped<&decode_f32_kernel<D, G, false, true>>(tp, tasks, sp, s);
+  }
+  return two ? launch_capped<&decode_f32_kernel<D, G, true, false>>(tp, tasks, sp, s)
+             : launch_capped<&decode_f32_kernel<D, G, false, false>>(tp, tasks, sp, s);
 }
 
 template <int D>
