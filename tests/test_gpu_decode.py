@@ -155,6 +155,43 @@ def test_pinned_host_tier_bit_identical(gpu):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+def test_max_seqlen_k_narrows_a_capacity_wide_table(gpu):
+    """The fa-style call with a block table sized to the cache's capacity (512
+    columns, as a serving engine keeps it) and rows of at most 300 tokens: with
+    max_seqlen_k = 300 only the first 19 columns are planned and read, and the
+    result equals a 19-column table's bit for bit (the capacity columns hold
+    ids past the cache, so reading one would poison its row). A row longer
+    than a smaller max_seqlen_k is a range error (NaN); the others match the
+    oracle."""
+    n, H, KVH, D, BS, C = 6, 32, 8, 128, 16, 64
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.bfloat16, 300, 21)
+    lens[:] = torch.tensor([300, 1, 0, 129, 288, 17], dtype=torch.int32)
+    W = bt.shape[1]
+    assert W == 19
+    wide = torch.full((n, 512), C + 7, dtype=torch.int32)
+    wide[:, :W] = bt
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    k, v = kv[..., :D], kv[..., D:]
+    scale = 1.0 / math.sqrt(D)
+    q_d, lens_d = q.to(gpu), lens.to(gpu)
+    o_wide, l_wide = ops.paged_decode(q_d, k, v, wide.to(gpu), lens_d, scale, max_seqlen_k=300)
+    o_narrow, l_narrow = ops.paged_decode(q_d, k, v, bt.to(gpu), lens_d, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(o_wide, o_narrow) and torch.equal(l_wide, l_narrow)
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    nz = lens > 0
+    tol = OUT_TOL_16BIT[torch.bfloat16]
+    assert_out_close(o_wide, ref_out, tol, tol, mask=nz)
+    assert_lse_close(l_wide, ref_lse, mask=nz)
+    # max_seqlen_k below a row's length: 200 tokens -> 13 columns; rows 0 and 4 overrun
+    o_short, l_short = ops.paged_decode(q_d, k, v, wide.to(gpu), lens_d, scale, max_seqlen_k=200)
+    torch.cuda.synchronize()
+    for r in (0, 4):
+        assert torch.isnan(o_short[r].float()).all() and torch.isnan(l_short[:, r]).all()
+    ok = torch.tensor([False, True, False, True, False, True])
+    assert_out_close(o_short, ref_out, tol, tol, mask=ok)
+
+
 def test_range_errors_poison_only_their_rows(gpu):
     """A table entry outside the cache, or a length beyond the table, turns
     that row into NaN without touching memory outside the cache; other rows

@@ -35,8 +35,8 @@ def test_decode_form_goes_to_hip_and_prefill_forms_to_flash_attention(monkeypatc
     hip_calls = []
 
     def fake_paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=None,
-                          row_order=None):
-        hip_calls.append((q.shape, block_table.shape))
+                          row_order=None, max_seqlen_k=None):
+        hip_calls.append((q.shape, block_table.shape, max_seqlen_k))
         return torch.zeros_like(q), torch.zeros(q.shape[1], q.shape[0])
 
     monkeypatch.setattr(backend.ops, "paged_decode", fake_paged_decode)
@@ -52,6 +52,7 @@ def test_decode_form_goes_to_hip_and_prefill_forms_to_flash_attention(monkeypatc
                     causal=False, block_table=bt, softcap=0.0, return_softmax_lse=True,
                     num_splits=1, fa_version=2)
     assert len(hip_calls) == 1 and not stub.calls
+    assert hip_calls[0][2] == 17  # max_seqlen_k reaches the decode (it narrows the table)
     # P rows: causal prefill over the paged cache (backend.py:317-327)
     OPS.fa(q=torch.zeros(7, H, D), k=kc, v=kc, cu_seqlens_q=torch.tensor([0, 4, 7]),
            max_seqlen_q=4, seqused_k=torch.tensor([20, 9]), max_seqlen_k=20,

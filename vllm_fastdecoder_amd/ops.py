@@ -756,6 +756,7 @@ def paged_decode(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     row_order: torch.Tensor | None = None,
+    max_seqlen_k: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """HBM-tier partial in vLLM's paged layout: the decode call of
     flash_attn_varlen_func at fastdecode/backend.py:306-314 (one query token
@@ -765,10 +766,21 @@ def paged_decode(
     interleaved [B, BS, KVH, 2D] cache). Returns out [n, H, D] (q's dtype
     unless `out` is given) and lse [H, n] float32. Rows with seqused_k == 0
     give out = 0 and lse = -inf (no FA row filtering is needed).
+
+    max_seqlen_k (flash_attn_varlen_func's argument: the longest row's token
+    count, an int the host knows): when given, only the table's first
+    ceil(max_seqlen_k / BS) columns are planned and read (a view with the
+    table's row stride), so a table sized to the cache's capacity costs no
+    more than one sized to the batch. A row longer than max_seqlen_k is then a
+    range error: its out and lse are NaN.
     """
     _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape,
              "key_cache/value_cache must be [B, BS, KVH, D]")
     B, BS, KVH, D = key_cache.shape
+    if max_seqlen_k is not None and block_table.dim() == 2:
+        cols = max(1, -(-int(max_seqlen_k) // BS))
+        if cols < block_table.shape[1]:
+            block_table = block_table[:, :cols]
     n, H = q.shape[0], q.shape[1]
     if out is None:
         out = torch.empty_like(q)
