@@ -99,7 +99,11 @@ int fd_abi_version(void);
  * num_blocks  blocks in the cache; a table entry outside [0, num_blocks) or
  *             lens[i] > bt_width*block_size is a device-side range error: the
  *             row's out and lse become NaN instead of reading out of bounds.
- * block_table int32 [n, >= bt_width], row stride bt_stride
+ * block_table int32 [n, >= bt_width], row stride bt_stride. The launch is
+ *             planned for rows of up to bt_width blocks: a caller whose table
+ *             is sized to the cache's capacity passes bt_width =
+ *             ceil(longest row / block_size) (flash-attn's max_seqlen_k) with
+ *             the full row stride, and pays nothing for the unused columns.
  * lens        int32 [n]
  * row_order   optional int32 [n] permutation of 0..n-1 (may be NULL): the order
  *             in which rows are scheduled. Results do not depend on it; passing
