@@ -134,12 +134,38 @@ int fd_paged_decode_partial(
     void* workspace, size_t workspace_bytes,
     void* stream);
 
-/* Bytes of workspace fd_paged_decode_partial needs for these sizes (the
- * block-range split partials), whatever the kv dtype and wherever the cache
- * lies: the largest need of the kernels such a call may take (an fp32 cache
- * streams twice the bytes per block and may split rows sooner). No
- * counterpart in the reference: its CPU kernel keeps per-thread scratch in
- * std::vector (cpu_attn.cpp:314-318). */
+/* fd_paged_decode_partial for a caller that knows the rows' token total
+ * (the sum of lens over the n rows; a serving step's scheduler has it on the
+ * host). Results are those of fd_paged_decode_partial; only the task sizes
+ * may differ. The launch plan otherwise sees only the table width, and rows
+ * of uneven length (mean fill of bt_width * block_size below 0.8) on the
+ * matrix-core kernel with 16 heads per task are then cut into tasks that
+ * fill three workgroups per CU, where rows of equal length keep whole-row
+ * tasks. total_tokens = 0: unknown (the same plan as
+ * fd_paged_decode_partial); a wrong total costs time, never correctness.
+ * No counterpart in the reference: its FlashAttention call plans from
+ * max_seqlen_k alone (fastdecode/backend.py:306-314). */
+int fd_paged_decode_partial_hint(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens, const int32_t* row_order,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    void* workspace, size_t workspace_bytes,
+    void* stream, int64_t total_tokens);
+
+/* Bytes of workspace fd_paged_decode_partial (and _hint, whatever its token
+ * total) needs for these sizes (the block-range split partials), whatever
+ * the kv dtype and wherever the cache lies: the largest need of the kernels
+ * such a call may take (an fp32 cache streams twice the bytes per block and
+ * may split rows sooner). No counterpart in the reference: its CPU kernel
+ * keeps per-thread scratch in std::vector (cpu_attn.cpp:314-318). */
 int fd_paged_decode_workspace_size(
     int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
     int32_t block_size, int32_t bt_width, size_t* bytes);
@@ -154,6 +180,8 @@ int fd_paged_decode_workspace_size(
  *               elements), else 0 (the generic kernel)
  *   host_tier   1 if a tier lies in pinned host memory (16-bit launches then
  *               take the VALU kernel)
+ *   total_tokens the rows' token total, as given to
+ *               fd_paged_decode_partial_hint (0: unknown)
  * FD_DECODE_KERNEL and FD_SPLIT_BLOCKS are honoured as in a launch. */
 #define FD_KERNEL_GENERIC 0 /* any layout, one wave per (sequence, head) */
 #define FD_KERNEL_VALU 1    /* 16-bit KV, vector ALUs */
@@ -167,12 +195,13 @@ typedef struct {
   int32_t passes;         /* tasks per (sequence, kv head, block range) */
   int32_t split_blocks;   /* 16-token tiles per task */
   int32_t max_splits;     /* tasks per row at most (> 1: a combine pass) */
-  int32_t capped;         /* 1: at most two workgroups per compute unit */
+  int32_t wg_cap;         /* workgroups per compute unit the launch allows at most
+                             (0: the kernel's own occupancy) */
 } FdDecodePlan;
 
 int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
                         int32_t block_size, int32_t bt_width, int32_t kv_dtype, int32_t aligned,
-                        int32_t host_tier, FdDecodePlan* plan);
+                        int32_t host_tier, int64_t total_tokens, FdDecodePlan* plan);
 
 /* Size of the device scratch behind fd_paged_decode_partial_noalloc. */
 #define FD_NOALLOC_SCRATCH_BYTES (32u << 20)

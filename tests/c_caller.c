@@ -130,7 +130,7 @@ int main(void) {
   if (fd_paged_decode_workspace_size(128, 32, 8, 128, 16, 256, &ws) != FD_OK) return 2;
 
   FdDecodePlan plan;
-  if (fd_decode_plan_info(128, 32, 8, 128, 16, 128, FD_BF16, 1, 0, &plan) != FD_OK) return 3;
+  if (fd_decode_plan_info(128, 32, 8, 128, 16, 128, FD_BF16, 1, 0, 0, &plan) != FD_OK) return 3;
   if (plan.kernel != FD_KERNEL_MM || plan.heads_per_task != 16 || plan.passes != 1) return 4;
 
   /* q == NULL: rejected on the host, with a message, nothing launched */

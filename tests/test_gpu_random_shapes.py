@@ -160,3 +160,49 @@ def test_random_two_tier_split_matches_oracle(gpu, i, monkeypatch):
         assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)])), "empty rows: lse not -inf"
     except AssertionError as e:
         raise AssertionError(f"{what}: {e}") from None
+
+
+@pytest.mark.parametrize("i", range(32))
+def test_random_shape_with_token_total_matches_oracle(gpu, i):
+    """paged_decode given the rows' token total (the planner's hint for rows
+    of uneven length), on random shapes in vLLM's layout: the true total in
+    even cases, a wrong one (1 token, or ten times the table) in odd ones. A
+    total steers only the task sizes: every case matches the oracle."""
+    H, KVH, D, BS, dtype, lens_l, _, out16, _ = _draw(300 + i)
+    n = len(lens_l)
+    nbs = [(L + BS - 1) // BS for L in lens_l]
+    C = sum(nbs) + 2
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=max(lens_l),
+                                          seed=300 + i)
+    lens[:] = torch.tensor(lens_l, dtype=torch.int32)
+    perm = torch.randperm(C, generator=torch.Generator().manual_seed(300 + i)).to(torch.int32)
+    bt.zero_()
+    pos = 0
+    for r, nb in enumerate(nbs):
+        bt[r, :nb] = perm[pos: pos + nb]
+        pos += nb
+    total = sum(lens_l) if i % 2 == 0 else (1 if i % 4 == 1 else 10 * n * bt.shape[1] * BS)
+    scale = 1.0 / math.sqrt(D)
+    info = ops.decode_plan_info(n, H, KVH, D, BS, bt.shape[1], dtype, total_tokens=total)
+    what = (f"case {i}: H={H} KVH={KVH} D={D} BS={BS} {dtype} lens={lens_l} total={total} "
+            f"out16={out16} plan={info}")
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q, kc, vc, bt, lens, scale)
+    kv = torch.cat([kc.transpose(1, 2), vc.transpose(1, 2)], dim=-1).contiguous().to(gpu)
+    out_dtype = dtype if out16 else torch.float32
+    out = torch.empty(n, H, D, dtype=out_dtype, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    ops.paged_decode(q.to(gpu), kv[..., :D], kv[..., D:], bt.to(gpu), lens.to(gpu), scale,
+                     out=out, lse=lse, total_tokens=total)
+    torch.cuda.synchronize()
+    nz = lens > 0
+    try:
+        if out16:
+            tol = OUT_TOL_16BIT[dtype]
+            assert_out_close(out, ref_out, tol, tol, mask=nz)
+        else:
+            assert_out_close(out, ref_out, 5e-5 if dtype == torch.float32 else 2e-3, mask=nz)
+        assert_lse_close(lse, ref_lse, mask=nz)
+        assert torch.all(out[~nz.to(gpu)] == 0), "empty rows: out not 0"
+        assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)])), "empty rows: lse not -inf"
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None

@@ -112,3 +112,38 @@ def test_bad_arguments_raise():
         plan(8, 30, 8, 128, 8)           # H not a multiple of KVH
     with pytest.raises(_lib.FdError):
         ops.decode_plan_info(8, 32, 8, 128, 16, -1, BF16)
+
+
+def test_token_total_without_a_device_keeps_the_plan():
+    """Without a GPU (no CU count) the token total changes nothing; a negative
+    total is an argument error."""
+    if torch.cuda.is_available():
+        pytest.skip("planner sees a device here")
+    a = ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16)
+    b = ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16, total_tokens=650_000)
+    assert a == b
+    with pytest.raises(Exception):
+        ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16, total_tokens=-1)
+
+
+@pytest.mark.gpu
+def test_token_total_steers_uneven_rows_to_the_slot_fill(gpu):
+    """On the device: 8 query heads over 1 kv head, batch 256, a 256-block
+    table. Rows filling 62 % of it on average take 64-block tasks at the
+    kernel's own three workgroups per CU (the slot fill); rows filling all of
+    it, or an unknown total, keep the model's whole-row tasks under the
+    two-per-CU cap. Other kernel families ignore the total."""
+    full = 256 * 256 * 16
+    base = ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16)
+    assert base["split_blocks"] == 256 and base["max_splits"] == 1 and base["wg_cap"] == 2
+    uneven = ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16,
+                                  total_tokens=int(0.62 * full))
+    assert uneven["kernel"] == "mm" and uneven["split_blocks"] == 64
+    assert uneven["max_splits"] == 4 and uneven["wg_cap"] == 0
+    assert ops.decode_plan_info(256, 8, 1, 128, 16, 256, torch.bfloat16, total_tokens=full) == base
+    mha = ops.decode_plan_info(16, 32, 32, 128, 16, 256, torch.bfloat16)
+    assert ops.decode_plan_info(16, 32, 32, 128, 16, 256, torch.bfloat16,
+                                total_tokens=int(0.5 * 16 * 256 * 16)) == mha
+    # the workspace query covers any total
+    need = ops.workspace_bytes(256, 8, 1, 128, 16, 256)
+    assert need >= 256 * 8 * 4 * 128 * 4

@@ -59,15 +59,28 @@ bool in_host_memory(const void* p) {
   return host;
 }
 
+// Mean fill of the table by the rows, from the caller's token total: the
+// rows' tokens over n * width * block_size, at most 1 (0: unknown).
+double row_fill(int64_t total_tokens, int32_t n, int64_t width, int32_t block_size) {
+  if (total_tokens <= 0 || n <= 0 || width <= 0) return 0.0;
+  const double cap = (double)n * (double)width * block_size;
+  return std::min(1.0, (double)total_tokens / cap);
+}
+
 // Validates a decode call over a.ntiers tiers (tiers already filled in),
 // completes `a` and launches it. Every check runs before the launch.
+// total_tokens: the rows' token total when the caller knows it (0: unknown);
+// it only steers the task sizes, never the results.
 int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_seq,
                int64_t q_stride_head, const int32_t* row_order, int32_t n, int32_t num_heads,
                int32_t num_kv_heads, int32_t head_size, int32_t block_size, float scale,
                int32_t kv_dtype, void* out, int64_t out_stride_seq, int64_t out_stride_head,
                int32_t out_dtype, float* lse, int64_t lse_stride_head, void* workspace,
-               size_t workspace_bytes, void* stream) {
+               size_t workspace_bytes, void* stream, int64_t total_tokens = 0) {
   if (n < 0) return set_error(FD_ERR_INVALID, "%s: n must be >= 0 (got %d)", who, n);
+  if (total_tokens < 0)
+    return set_error(FD_ERR_INVALID, "%s: total_tokens must be >= 0 (got %lld)", who,
+                     (long long)total_tokens);
   if (num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return set_error(FD_ERR_INVALID,
                      "%s: num_heads must be a multiple of num_kv_heads (%d, %d)", who, num_heads,
@@ -109,8 +122,9 @@ int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_s
               ((int64_t)(block_size - 1) * kt.st + head_size) * (kv_dtype == FD_F32 ? 4 : 2) <
                   (1ll << 31);
   }
+  const double fill = row_fill(total_tokens, n, width, block_size);
   SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size,
-                             (int32_t)width, kv_dtype, aligned);
+                             (int32_t)width, kv_dtype, aligned, true, fill);
   // Over the link the matrix-core kernels' K tiles (16 token rows of 16 bytes
   // per lane group) read slower than the VALU kernel's whole rows (measured
   // on a GQA-4 host tier: 47.9 against 55.9 GB/s; in HBM the two are within
@@ -119,7 +133,7 @@ int run_decode(DecodeArgs& a, const char* who, const void* q, int64_t q_stride_s
   for (int t = 0; (sp.mfma || sp.mm) && t < a.ntiers; ++t) host = host || in_host_memory(a.tier[t].k);
   if (host)
     sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, (int32_t)width, kv_dtype,
-                     aligned, false);
+                     aligned, false, fill);
   const size_t need = decode_workspace_bytes(sp, n, num_heads, head_size);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
     return set_error(FD_ERR_WORKSPACE,
@@ -157,7 +171,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 7; }
+int fd_abi_version(void) { return 8; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -176,6 +190,9 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
     const SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width,
                                      dts[c], true, c == 0);
     most = std::max(most, decode_workspace_bytes(sp, n, num_heads, head_size));
+    // what a token total may make of it (fd_paged_decode_partial_hint)
+    most = std::max(most, fill_workspace_bound(sp, n, num_heads, head_size, block_size,
+                                               bt_width));
   }
   *bytes = most;
   return FD_OK;
@@ -183,20 +200,21 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
 
 int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
                         int32_t block_size, int32_t bt_width, int32_t kv_dtype, int32_t aligned,
-                        int32_t host_tier, FdDecodePlan* plan) {
+                        int32_t host_tier, int64_t total_tokens, FdDecodePlan* plan) {
   if (plan == nullptr) return set_error(FD_ERR_INVALID, "plan_info: plan is NULL");
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
-      head_size <= 0 || block_size <= 0 || bt_width < 0)
+      head_size <= 0 || block_size <= 0 || bt_width < 0 || total_tokens < 0)
     return set_error(FD_ERR_INVALID, "plan_info: bad sizes");
+  const double fill = row_fill(total_tokens, n, bt_width, block_size);
   if (kv_dtype != FD_F16 && kv_dtype != FD_BF16 && kv_dtype != FD_F32)
     return set_error(FD_ERR_INVALID, "plan_info: unsupported kv dtype %d", kv_dtype);
   // the same two-step choice as run_decode: a tier in pinned host memory
   // re-plans 16-bit launches without the matrix-core kernels
   SplitPlan sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width, kv_dtype,
-                             aligned != 0);
+                             aligned != 0, true, fill);
   if (host_tier != 0 && (sp.mfma || sp.mm))
     sp = plan_decode(n, num_heads, num_kv_heads, head_size, block_size, bt_width, kv_dtype,
-                     aligned != 0, false);
+                     aligned != 0, false, fill);
   plan->kernel = !sp.fast ? FD_KERNEL_GENERIC
                  : kv_dtype == FD_F32 ? FD_KERNEL_F32
                  : sp.mm ? FD_KERNEL_MM
@@ -206,7 +224,7 @@ int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int3
   plan->passes = sp.fast ? sp.passes : 1;
   plan->split_blocks = sp.split_blocks;
   plan->max_splits = sp.max_splits;
-  plan->capped = sp.fast && sp.cap_occupancy ? 1 : 0;
+  plan->wg_cap = sp.fast ? sp.wg_cap : 0;
   return FD_OK;
 }
 
@@ -229,6 +247,25 @@ int fd_paged_decode_partial(const void* q, int64_t q_stride_seq, int64_t q_strid
                     num_kv_heads, head_size, block_size, scale, kv_dtype, out, out_stride_seq,
                     out_stride_head, out_dtype, lse, lse_stride_head, workspace,
                     workspace_bytes, stream);
+}
+
+int fd_paged_decode_partial_hint(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, int64_t kv_stride_block, int64_t kv_stride_head,
+    int64_t kv_stride_token, int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+    int32_t bt_width, const int32_t* lens, const int32_t* row_order, int32_t n,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_size, int32_t block_size, float scale,
+    int32_t kv_dtype, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype, float* lse, int64_t lse_stride_head, void* workspace,
+    size_t workspace_bytes, void* stream, int64_t total_tokens) {
+  DecodeArgs a{};
+  a.tier[0] = KvTier{k_cache, v_cache, kv_stride_block, kv_stride_head, kv_stride_token,
+                     num_blocks, block_table, bt_stride, bt_width, lens};
+  a.ntiers = 1;
+  return run_decode(a, "decode", q, q_stride_seq, q_stride_head, row_order, n, num_heads,
+                    num_kv_heads, head_size, block_size, scale, kv_dtype, out, out_stride_seq,
+                    out_stride_head, out_dtype, lse, lse_stride_head, workspace,
+                    workspace_bytes, stream, total_tokens);
 }
 
 int fd_split_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,

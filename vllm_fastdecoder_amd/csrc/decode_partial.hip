@@ -217,35 +217,128 @@ static int device_cus() {
   return cus;
 }
 
-// Dynamic LDS that leaves room for at most two workgroups of `kernel` per CU
-// (the reservation is never touched), or 0 when the kernel's own LDS already
-// keeps it there or the reservation would not fit one workgroup's limit.
-// Measured on MI355X: with tasks of 32+ blocks, two workgroups per CU (8
-// waves, one block in flight each) already saturate HBM, and the fewer
+// LDS of the current device: per CU and the most one workgroup may take
+// (cached per device; 0 if unknown).
+static void device_lds(int dev, int* per_cu, int* per_wg) {
+  static std::atomic<int> cu_cache[kMaxDevices] = {}, wg_cache[kMaxDevices] = {};
+  int cu = cu_cache[dev].load(std::memory_order_relaxed) - 1;
+  int wg = wg_cache[dev].load(std::memory_order_relaxed) - 1;
+  if (cu < 0 || wg < 0) {
+    if (hipDeviceGetAttribute(&cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) !=
+            hipSuccess ||
+        hipDeviceGetAttribute(&wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+      cu = wg = 0;
+    cu_cache[dev].store(cu + 1, std::memory_order_relaxed);
+    wg_cache[dev].store(wg + 1, std::memory_order_relaxed);
+  }
+  *per_cu = cu;
+  *per_wg = wg;
+}
+
+// Dynamic LDS that leaves room for at most `wgs` workgroups of `kernel` per
+// CU (the reservation is never touched), or 0 when the kernel's own LDS
+// already keeps it there or the reservation would not fit one workgroup's
+// limit. Measured on MI355X: with tasks of 32+ blocks, two workgroups per CU
+// (8 waves, one block in flight each) already saturate HBM, and the fewer
 // concurrent streams read faster (+1 to +6 % over the natural 3-4 per CU);
-// short tasks want the extra workgroups to hide their
-// start-up latency, so they are left uncapped. `cache` holds the result + 1
-// per device (0 = not computed yet).
-unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache) {
+// short tasks want the extra workgroups to hide their start-up latency, so
+// they are left uncapped. `cache` holds the kernel's static LDS + 1 per
+// device (0 = not read yet).
+unsigned cap_lds(const void* kernel, int wgs, std::atomic<int>* cache) {
+  int dev = 0;
+  if (wgs <= 0 || hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  int stat = cache[dev].load(std::memory_order_relaxed) - 1;
+  if (stat < 0) {
+    hipFuncAttributes fa{};
+    // unknown: as if the kernel's own LDS already capped it (no reservation)
+    stat = hipFuncGetAttributes(&fa, kernel) == hipSuccess ? (int)fa.sharedSizeBytes : 1 << 30;
+    cache[dev].store(stat + 1, std::memory_order_relaxed);
+  }
+  int per_cu = 0, per_wg = 0;
+  device_lds(dev, &per_cu, &per_wg);
+  // more than 1 / (wgs + 1) of the CU: wgs workgroups fit, one more does not
+  const int need = per_cu / (wgs + 1) + 1024;
+  return per_cu > 0 && need > stat && need <= per_wg ? (unsigned)(need - stat) : 0u;
+}
+
+int natural_wgs_per_cu(const void* kernel, std::atomic<int>* cache) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  int v = cache[dev].load(std::memory_order_relaxed);
-  if (v > 0) return (unsigned)(v - 1);
-  int per_cu = 0, per_wg = 0;
-  hipFuncAttributes fa{};
-  v = 0;
-  if (hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) ==
-          hipSuccess &&
-      hipDeviceGetAttribute(&per_wg, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) ==
-          hipSuccess &&
-      hipFuncGetAttributes(&fa, kernel) == hipSuccess) {
-    const int stat = (int)fa.sharedSizeBytes;
-    const int need = per_cu / 3 + 1024;  // more than a third of the CU: two fit, three do not
-    if (need > stat && need <= per_wg) v = need - stat;
-  }
-  cache[dev].store(v + 1, std::memory_order_relaxed);
-  return (unsigned)v;
+  const int v = cache[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v - 1;
+  int wgs = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&wgs, kernel, kWave * kWavesPerTask, 0) !=
+      hipSuccess)
+    wgs = 0;
+  cache[dev].store(wgs + 1, std::memory_order_relaxed);
+  return wgs;
 }
+
+namespace {
+
+// The tiled kernel family the plan selects, for a launch or (with the plan's
+// occupancy query set) for its occupancy.
+hipError_t dispatch_tiled(const TiledParams& tp, unsigned tasks, const SplitPlan& sp,
+                          int32_t kv_dtype, int32_t D, bool two, hipStream_t s) {
+  const int G = sp.kernel_g;  // the kernel's head slots per task
+  return kv_dtype == FD_F32 ? launch_f32(tp, tasks, sp, sp.kernel_d, G, two, s)
+         : sp.mm            ? launch_mm(tp, tasks, sp, kv_dtype, D, two, s)
+         : sp.mfma          ? launch_mfma(tp, tasks, sp, kv_dtype, D, G, two, s)
+                            : launch_valu(tp, tasks, sp, kv_dtype, sp.kernel_d, G, two, s);
+}
+
+// Workgroups per CU of the (single-tier, separate K / V loads) kernel the
+// plan selects; 0 when no device answers.
+int tiled_wgs_per_cu(const SplitPlan& sp, int32_t kv_dtype, int32_t D) {
+  SplitPlan q = sp;
+  int wgs = 0;
+  q.occupancy_query = &wgs;
+  TiledParams tp{};
+  tp.D = D;
+  return dispatch_tiled(tp, 0, q, kv_dtype, D, false, nullptr) == hipSuccess ? wgs : 0;
+}
+
+// Tasks a launch is expected to run with S tasks per full row when its rows
+// fill `fill` of the table width on average (a row of fill x has ceil(x S)
+// tasks; about fill * S + 1/2 per row).
+double expected_tasks(int32_t n, int32_t kv_tasks, int64_t S, double fill) {
+  return (double)n * kv_tasks * (S <= 1 ? 1.0 : std::min((double)S, fill * S + 0.5));
+}
+
+constexpr int kFillPerCu = 3;          // workgroups per CU the slot fill runs at
+constexpr int32_t kMaxFillSplits = 8;  // nor splits a row into more tasks than this
+constexpr double kMaxFillRows = 0.8;   // mean row fill below which rows count as uneven
+constexpr double kMinFillSlots = 0.6;  // share of the slots a slot fill uses at least
+
+// The slot fill of the matrix-core kernel with one 16-head column group, for
+// rows of uneven length (mean fill of the table width known from the caller
+// and below 0.8): blocks per task such that one round of three workgroups per
+// CU holds every task, at least 60 % of those slots are used and no row
+// splits more than eight ways, or 0 when no task size does; the coarsest
+// such size wins. One workgroup of this kernel is a slow stream (its
+// per-block chain: scores MFMAs, the cross-row max, the LDS round trip of V,
+// the P.V MFMAs), so uneven rows leave the CUs holding the longest ones
+// working long after the rest; three per CU, each with a share of the work,
+// end together. Measured on MI355X (bf16, D = 128, HIP graph replay): 8 query
+// heads on 1 kv head, batch 256, rows of U[1024, 4096] tokens: 61.6 us at
+// 64-block tasks three per CU against 67.8 us unsplit (the model's choice);
+// rows of U[256, 4096]: 57.8 against 63.9 us. Rows of equal length lose
+// instead (86.7 -> 101.2 us at 4096 tokens: every row splits into whole
+// tasks and a second round returns), which is why the fill needs the caller's
+// length total.
+int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots, double fill) {
+  const int64_t W = wt > 0 ? wt : 1;
+  for (int32_t sb = kMaxSplitBlocks; sb >= kTileTokens; sb /= 2) {
+    const int64_t S = (W + sb - 1) / sb;
+    if (S > kMaxFillSplits) break;
+    const double tasks = expected_tasks(n, kv_tasks, S, fill);
+    if (tasks > (double)slots) break;  // finer sizes only add tasks
+    if (tasks > kMinFillSlots * (double)slots) return sb;
+  }
+  return 0;
+}
+
+}  // namespace
 
 // Blocks per task (16 .. 256) from a launch-time model. Only the shapes are
 // known on the host (row lengths live on the device), so rows are taken as
@@ -292,7 +385,8 @@ int32_t model_split_blocks(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t
 }
 
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
-                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix) {
+                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix,
+                      double fill) {
   SplitPlan sp{};
   sp.passes = 1;
   const int G = KVH > 0 ? H / KVH : 0;
@@ -363,13 +457,34 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
   int sb = split_blocks_override();
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
-  // each pass streams the blocks once more: model it as that many kv heads
-  if (sb <= 0) sb = model_split_blocks(n, H, KVH * sp.passes, D, kTileTokens, wt, f32 ? 4 : 2);
+  // each pass streams the blocks once more: count it as that many kv heads
+  const int32_t kv_tasks = KVH * sp.passes;
+  const int elt = f32 ? 4 : 2;
+  bool filled = false;
+  if (sb <= 0 && fill > 0.0 && fill < kMaxFillRows && sp.mm && sp.kernel_g == 16 && cus > 0) {
+    // uneven rows on the one-column-group matrix-core kernel: the slot fill
+    sb = fill_split_blocks(n, kv_tasks, wt, (int64_t)kFillPerCu * cus, fill);
+    filled = sb > 0;
+  }
+  if (sb <= 0) sb = model_split_blocks(n, H, kv_tasks, D, kTileTokens, wt, elt);
   sp.split_blocks = sb;
   sp.max_splits = wt > 0 ? (wt + sb - 1) / sb : 1;
-  const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=0: natural occupancy (tuning)
-  sp.cap_occupancy = sb >= 32 && !(cap != nullptr && strcmp(cap, "0") == 0);
+  // The slot fill runs at three workgroups per CU (a cap where the kernel
+  // would hold more; its own occupancy where that is three).
+  sp.wg_cap = filled ? (tiled_wgs_per_cu(sp, kv_dtype, D) > kFillPerCu ? kFillPerCu : 0)
+                     : sb >= 32 ? 2 : 0;
+  const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=<k>: at most k per CU, 0 none (tuning)
+  if (cap != nullptr && *cap != 0) sp.wg_cap = std::max(0, atoi(cap));
   return sp;
+}
+
+size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t D, int32_t BS,
+                            int32_t bt_width) {
+  if (!sp.fast || !sp.mm || sp.kernel_g != 16 || BS % kTileTokens != 0 || bt_width <= 0) return 0;
+  const int64_t wt = (int64_t)bt_width * (BS / kTileTokens);
+  SplitPlan b = sp;
+  b.max_splits = (int32_t)std::min<int64_t>(kMaxFillSplits, (wt + kTileTokens - 1) / kTileTokens);
+  return decode_workspace_bytes(b, n, H, D);
 }
 
 size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H, int32_t D) {
@@ -464,11 +579,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   }
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
-  const int G = sp.kernel_g;  // the kernel's head slots per task
-  hipError_t e = f32       ? launch_f32(tp, (unsigned)tasks, sp, sp.kernel_d, G, two, s)
-                 : sp.mm   ? launch_mm(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s)
-                 : sp.mfma ? launch_mfma(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, G, two, s)
-                           : launch_valu(tp, (unsigned)tasks, sp, a.kv_dtype, sp.kernel_d, G, two, s);
+  hipError_t e = dispatch_tiled(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");
   if (sp.max_splits > 1) {
     const int64_t threads = (int64_t)a.n * a.H * (a.D / 4);

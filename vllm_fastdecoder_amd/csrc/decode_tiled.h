@@ -94,20 +94,29 @@ hipError_t launch_mm(const TiledParams& tp, unsigned tasks, const SplitPlan& sp,
 hipError_t launch_f32(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, int D, int G,
                       bool two_tiers, hipStream_t s);
 
-// Dynamic LDS that caps `kernel` at two workgroups per CU (decode_partial.hip).
-unsigned two_per_cu_lds(const void* kernel, std::atomic<int>* cache);
+// Dynamic LDS that caps `kernel` at `wgs` workgroups per CU (decode_partial.hip).
+unsigned cap_lds(const void* kernel, int wgs, std::atomic<int>* cache);
+// Workgroups of `kernel` one CU holds at once without a cap, 0 if unknown
+// (decode_partial.hip).
+int natural_wgs_per_cu(const void* kernel, std::atomic<int>* cache);
 
 // Launches `Kernel` with the occupancy cap when the plan asks for it. The
 // kernel is a template argument so that each kernel has its own settings
 // cache: the reserve depends on the kernel's static LDS (every kernel here
 // has the type void(TiledParams), so a cache keyed by the pointer's type
-// would hand the first kernel's reserve to all the others).
+// would hand the first kernel's reserve to all the others). A plan with an
+// occupancy query launches nothing: it only reports the kernel's occupancy.
 template <void (*Kernel)(TiledParams)>
 hipError_t launch_capped(const TiledParams& tp, unsigned tasks, const SplitPlan& sp,
                          hipStream_t s) {
+  if (sp.occupancy_query != nullptr) {
+    static std::atomic<int> occupancy[kMaxDevices] = {};
+    *sp.occupancy_query = natural_wgs_per_cu(reinterpret_cast<const void*>(Kernel), occupancy);
+    return hipSuccess;
+  }
   static std::atomic<int> cache[kMaxDevices] = {};
   const unsigned lds =
-      sp.cap_occupancy ? two_per_cu_lds(reinterpret_cast<const void*>(Kernel), cache) : 0;
+      sp.wg_cap > 0 ? cap_lds(reinterpret_cast<const void*>(Kernel), sp.wg_cap, cache) : 0;
   hipLaunchKernelGGL(Kernel, dim3(tasks), dim3(kWave * kWavesPerTask), lds, s, tp);
   return hipGetLastError();
 }

@@ -207,19 +207,29 @@ struct SplitPlan {
   bool fast;             // the tiled kernel applies (else the generic one)
   bool mfma;             // grouped-query scores on the matrix cores (G >= 4 at D = 256)
   bool mm;               // scores and P.V on the matrix cores (G >= 4, D <= 128)
-  bool cap_occupancy;    // long tasks: at most two workgroups per CU
+  int32_t wg_cap;        // workgroups per CU the launch allows at most (0: the kernel's own
+                         // occupancy); enforced by reserving LDS
   int32_t kernel_g;      // head slots per task of the tiled kernel: 1, 2, 4, 8, 16, 32 or 64
   int32_t kernel_d;      // head size the tiled kernel is built for: 64, 128 or 256
   int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
                          // kernel_g), each over the same blocks
+  int* occupancy_query;  // planner only: when set, the tiled launchers store the selected
+                         // kernel's workgroups per CU there instead of launching it
 };
 
 // matrix: the matrix-core kernels may be used (false when a tier lies in
 // pinned host memory, which the VALU kernel reads faster over the link).
+// fill: the rows' mean length over bt_width * BS when the caller knows it
+// (0: unknown).
 SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
-                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix = true);
+                      int32_t bt_width, int32_t kv_dtype, bool aligned, bool matrix = true,
+                      double fill = 0.0);
 size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H,
                               int32_t D);
+// Workspace the slot fill may need for a plan of these sizes whatever the
+// rows' token total (0 when the fill cannot apply to it).
+size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t D, int32_t BS,
+                            int32_t bt_width);
 int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s);
 
 struct MergeArgs {

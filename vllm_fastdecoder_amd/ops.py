@@ -121,18 +121,23 @@ _WS_SIZES: dict = {}
 
 
 def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtype: torch.dtype,
-                     aligned: bool = True, host_tier: bool = False) -> dict:
+                     aligned: bool = True, host_tier: bool = False,
+                     total_tokens: int | None = None) -> dict:
     """The kernel a decode launch of these sizes takes on the current device and
     how it is cut into tasks (fd_decode_plan_info): {"kernel": "valu" | "mm" |
     "mfma" | "f32" | "generic", "heads_per_task", "passes", "split_blocks",
-    "max_splits", "capped"}. Honours FD_DECODE_KERNEL / FD_SPLIT_BLOCKS."""
+    "max_splits", "wg_cap" (workgroups per CU the launch allows, 0 = the
+    kernel's own occupancy), "capped" (wg_cap > 0)}. total_tokens: the rows'
+    token total a paged_decode call is given (None: unknown). Honours
+    FD_DECODE_KERNEL / FD_SPLIT_BLOCKS / FD_WG_CAP."""
     plan = _lib.FdDecodePlan()
     _lib.check(_lib.load_lib().fd_decode_plan_info(n, H, KVH, D, BS, width, _DT[dtype],
                                                    int(aligned), int(host_tier),
+                                                   int(total_tokens or 0),
                                                    ctypes.byref(plan)))
     return {"kernel": _lib.FD_KERNEL_NAMES[plan.kernel], "heads_per_task": plan.heads_per_task,
             "passes": plan.passes, "split_blocks": plan.split_blocks,
-            "max_splits": plan.max_splits, "capped": bool(plan.capped)}
+            "max_splits": plan.max_splits, "wg_cap": plan.wg_cap, "capped": plan.wg_cap > 0}
 
 
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
@@ -166,10 +171,13 @@ def paged_decode_partial(
     lse: torch.Tensor,
     workspace: torch.Tensor | None = None,
     row_order: torch.Tensor | None = None,
+    total_tokens: int | None = None,
 ) -> None:
     """Layout-generic entry: kv_strides = (block, head, token) in elements.
     row_order: optional int32 [n] permutation scheduling the rows (e.g.
-    longest_first(lens)); results do not depend on it."""
+    longest_first(lens)); results do not depend on it. total_tokens: the
+    rows' token total when the caller knows it on the host
+    (fd_paged_decode_partial_hint); it steers the task sizes only."""
     _require(q.is_cuda and out.is_cuda and lse.is_cuda, "q, out and lse must be on the GPU")
     _require(q.dim() == 3 and out.shape == q.shape, "q and out must be [n, H, D] of one shape")
     n, H, D = q.shape
@@ -207,22 +215,24 @@ def paged_decode_partial(
         row_order = _on_device(row_order, dev).contiguous()
         order_ptr = row_order.data_ptr()
     lib = _lib.load_lib()
-    _lib.check(
-        lib.fd_paged_decode_partial(
-            q.data_ptr(), q.stride(0), q.stride(1),
-            device_ptr(k_cache), device_ptr(v_cache),
-            kv_strides[0], kv_strides[1], kv_strides[2],
-            num_blocks,
-            bt.data_ptr(), bt.stride(0), W,
-            ln.data_ptr(), order_ptr,
-            n, H, num_kv_heads, D,
-            block_size, float(scale), kv_dt,
-            out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
-            lse.data_ptr(), lse.stride(0),
-            ws_ptr, ws_len,
-            _stream_for(q),
-        )
+    args = (
+        q.data_ptr(), q.stride(0), q.stride(1),
+        device_ptr(k_cache), device_ptr(v_cache),
+        kv_strides[0], kv_strides[1], kv_strides[2],
+        num_blocks,
+        bt.data_ptr(), bt.stride(0), W,
+        ln.data_ptr(), order_ptr,
+        n, H, num_kv_heads, D,
+        block_size, float(scale), kv_dt,
+        out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
+        lse.data_ptr(), lse.stride(0),
+        ws_ptr, ws_len,
+        _stream_for(q),
     )
+    if total_tokens is None:
+        _lib.check(lib.fd_paged_decode_partial(*args))
+    else:
+        _lib.check(lib.fd_paged_decode_partial_hint(*args, int(total_tokens)))
 
 
 def _tier(k_cache, v_cache, strides, num_blocks, block_table, lens, n, dev, what):
@@ -757,6 +767,7 @@ def paged_decode(
     lse: torch.Tensor | None = None,
     row_order: torch.Tensor | None = None,
     max_seqlen_k: int | None = None,
+    total_tokens: int | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """HBM-tier partial in vLLM's paged layout: the decode call of
     flash_attn_varlen_func at fastdecode/backend.py:306-314 (one query token
@@ -773,6 +784,11 @@ def paged_decode(
     table's row stride), so a table sized to the cache's capacity costs no
     more than one sized to the batch. A row longer than max_seqlen_k is then a
     range error: its out and lse are NaN.
+
+    total_tokens (this build's addition: the sum of seqused_k, which a serving
+    step's scheduler knows on the host): lets the launch plan tell rows of
+    uneven length from equal ones, which want different task sizes. Results
+    do not depend on it.
     """
     _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape,
              "key_cache/value_cache must be [B, BS, KVH, D]")
@@ -791,6 +807,7 @@ def paged_decode(
         q, key_cache, value_cache,
         (key_cache.stride(0), key_cache.stride(2), key_cache.stride(1)),
         B, BS, KVH, block_table, seqused_k, softmax_scale, out, lse, row_order=row_order,
+        total_tokens=total_tokens,
     )
     return out, lse
 
