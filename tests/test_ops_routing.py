@@ -35,7 +35,7 @@ def test_decode_form_goes_to_hip_and_prefill_forms_to_flash_attention(monkeypatc
     hip_calls = []
 
     def fake_paged_decode(q, k, v, block_table, seqused_k, softmax_scale, out=None,
-                          row_order=None, max_seqlen_k=None):
+                          row_order=None, max_seqlen_k=None, total_tokens=None):
         hip_calls.append((q.shape, block_table.shape, max_seqlen_k))
         return torch.zeros_like(q), torch.zeros(q.shape[1], q.shape[0])
 

@@ -306,6 +306,7 @@ double expected_tasks(int32_t n, int32_t kv_tasks, int64_t S, double fill) {
 }
 
 constexpr int kFillPerCu = 3;          // workgroups per CU the slot fill runs at
+constexpr int32_t kMinFillBlocks = 16;  // smallest task the slot fill makes (blocks)
 constexpr int32_t kMaxFillSplits = 8;  // nor splits a row into more tasks than this
 constexpr double kMaxFillRows = 0.8;   // mean row fill below which rows count as uneven
 constexpr double kMinFillSlots = 0.6;  // share of the slots a slot fill uses at least
@@ -319,16 +320,19 @@ constexpr double kMinFillSlots = 0.6;  // share of the slots a slot fill uses at
 // per-block chain: scores MFMAs, the cross-row max, the LDS round trip of V,
 // the P.V MFMAs), so uneven rows leave the CUs holding the longest ones
 // working long after the rest; three per CU, each with a share of the work,
-// end together. Measured on MI355X (bf16, D = 128, HIP graph replay): 8 query
-// heads on 1 kv head, batch 256, rows of U[1024, 4096] tokens: 61.6 us at
-// 64-block tasks three per CU against 67.8 us unsplit (the model's choice);
-// rows of U[256, 4096]: 57.8 against 63.9 us. Rows of equal length lose
-// instead (86.7 -> 101.2 us at 4096 tokens: every row splits into whole
-// tasks and a second round returns), which is why the fill needs the caller's
-// length total.
+// end together. Measured on MI355X (bf16, HIP graph replay, the same call
+// with and without the total): 8 query heads on 1 kv head, batch 256, rows
+// of U[1024, 4096] tokens 67.4 -> 61.7 us (64-block tasks, three per CU,
+// against whole rows under the two-per-CU cap), rows of U[256, 4096] 63.7 ->
+// 57.1 us; over 17 shapes of 8/1, 12/2, 28/4, 32/8, 64/8 at D = 128 and 14/2
+// at D = 64 the fill took +8 to +17 % where it applied, for rows of
+// U[L/4, L] and U[L/16, L], and left the others within 0.5 %. Rows of equal
+// length lose under it (86.7 -> 101.2 us at 4096 tokens: every row splits
+// into whole tasks and a second round returns); they keep the model's plan,
+// which is why the fill needs the caller's total.
 int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots, double fill) {
   const int64_t W = wt > 0 ? wt : 1;
-  for (int32_t sb = kMaxSplitBlocks; sb >= kTileTokens; sb /= 2) {
+  for (int32_t sb = kMaxSplitBlocks; sb >= kMinFillBlocks; sb /= 2) {
     const int64_t S = (W + sb - 1) / sb;
     if (S > kMaxFillSplits) break;
     const double tasks = expected_tasks(n, kv_tasks, S, fill);
@@ -483,7 +487,8 @@ size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t D
   if (!sp.fast || !sp.mm || sp.kernel_g != 16 || BS % kTileTokens != 0 || bt_width <= 0) return 0;
   const int64_t wt = (int64_t)bt_width * (BS / kTileTokens);
   SplitPlan b = sp;
-  b.max_splits = (int32_t)std::min<int64_t>(kMaxFillSplits, (wt + kTileTokens - 1) / kTileTokens);
+  b.max_splits =
+      (int32_t)std::min<int64_t>(kMaxFillSplits, (wt + kMinFillBlocks - 1) / kMinFillBlocks);
   return decode_workspace_bytes(b, n, H, D);
 }
 

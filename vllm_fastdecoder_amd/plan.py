@@ -55,6 +55,7 @@ class HostPlan:
     s_gpu_bt: torch.Tensor  # [nS, Wg] int32 (HBM-tier block ids, compacted)
     s_gpu_lens: torch.Tensor  # [nS] int32
     s_max_gpu_len: int
+    s_gpu_tokens: int  # sum of s_gpu_lens (the decode launch's token-total hint)
     s_cpu_bt: torch.Tensor  # [nS, Wc] int32 (host-tier-relative ids, compacted)
     s_cpu_lens: torch.Tensor  # [nS] int32
     # F
@@ -208,6 +209,7 @@ def build_host_plan(
         s_gpu_bt=compact_rows(ids[s_req], in_hbm[s_req], 0, pad_to=GPU_TABLE_PAD),
         s_gpu_lens=t(s_gpu_lens),
         s_max_gpu_len=int(s_gpu_lens.max()) if s_gpu_lens.size else 0,
+        s_gpu_tokens=int(s_gpu_lens.sum()),
         s_cpu_bt=compact_rows(ids[s_req], in_host[s_req], G),
         s_cpu_lens=t(s_cpu_lens),
         f_tok=t(_token_runs(qsl[f_req], f_q)),
