@@ -72,6 +72,29 @@ def test_paged_decode_in_a_graph(gpu, split, monkeypatch):
     _replays(gpu, q, step, [out, lse], ws_bytes=ws)
 
 
+def test_paged_decode_with_token_total_in_a_graph(gpu):
+    """The token-total hint in a graph: rows of uneven length on the
+    matrix-core kernel take the slot fill's split tasks and the combine; each
+    replay matches an eager call bit for bit."""
+    w = cases.Workload("graph", 128, 8, 1, 128, 16, torch.bfloat16, 1024, 4096, None, 17)
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    total = int(lens.sum())
+    info = ops.decode_plan_info(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1], w.dtype,
+                                total_tokens=total)
+    assert info["max_splits"] > 1, info
+    kc, vc, _kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    bt_d, lens_d = bt.to(gpu), lens.to(gpu)
+    out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=gpu)
+
+    def step():
+        ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse, total_tokens=total)
+
+    ws = ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1])
+    _replays(gpu, q, step, [out, lse], ws_bytes=ws)
+
+
 def test_fused_split_in_a_graph(gpu):
     c = two_tier_case(10, 32, 32, 128, torch.float16, seed=17, dev=gpu)
     q = c["q"].to(gpu)
