@@ -5,7 +5,8 @@
  * fp32 data, checked against a direct double-precision computation. Built
  * with -DWITH_GPU (and the HIP runtime API, which is C), it also runs the
  * GPU entry point on device copies of a larger fp32 case (16-token blocks:
- * the tiled fp32 kernel) and checks it the same way.
+ * the tiled fp32 kernel), with and without the rows' token total, and checks
+ * it the same way.
  * Exit status 0 = every check passed; otherwise the number of the check. */
 #include <math.h>
 #include <stdint.h>
@@ -105,17 +106,34 @@ static int gpu_case(void) {
   if (hipDeviceSynchronize() || hipMemcpy(gout, dout, sizeof gout, hipMemcpyDeviceToHost) ||
       hipMemcpy(glse, dlse, sizeof glse, hipMemcpyDeviceToHost))
     return 5;
-  for (int i = 0; i < GN; ++i)
-    for (int h = 0; h < GH; ++h) {
-      if (lens[i] == 0) {
-        for (int d = 0; d < GD; ++d)
-          if (gout[i][h][d] != 0.0f) return 6;
-        if (!(isinf(glse[h][i]) && glse[h][i] < 0)) return 7;
-      } else if (check_row(gq[i][h], &gk[0][0][0][0], &gv[0][0][0][0], bt[i], lens[i],
-                           h / (GH / GKVH), GKVH, GBS, GD, scale, gout[i][h], glse[h][i])) {
-        return 8;
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int i = 0; i < GN; ++i)
+      for (int h = 0; h < GH; ++h) {
+        if (lens[i] == 0) {
+          for (int d = 0; d < GD; ++d)
+            if (gout[i][h][d] != 0.0f) return 6;
+          if (!(isinf(glse[h][i]) && glse[h][i] < 0)) return 7;
+        } else if (check_row(gq[i][h], &gk[0][0][0][0], &gv[0][0][0][0], bt[i], lens[i],
+                             h / (GH / GKVH), GKVH, GBS, GD, scale, gout[i][h], glse[h][i])) {
+          return 8;
+        }
       }
+    if (pass == 1) break;
+    /* again through the entry point that takes the rows' token total */
+    memset(gout, 0, sizeof gout);
+    if (hipMemcpy(dout, gout, sizeof gout, hipMemcpyHostToDevice)) return 3;
+    if (fd_paged_decode_partial_hint(dq, GH * GD, GD, dk, dv, GKVH * GBS * GD, GBS * GD, GD, GC,
+                                     (const int32_t*)dbt, GW, GW, (const int32_t*)dlens, NULL,
+                                     GN, GH, GKVH, GD, GBS, scale, FD_F32, dout, GH * GD, GD,
+                                     FD_F32, (float*)dlse, GN, dws, ws, NULL,
+                                     (int64_t)lens[0] + lens[1] + lens[2]) != FD_OK) {
+      fprintf(stderr, "%s\n", fd_last_error());
+      return 9;
     }
+    if (hipDeviceSynchronize() || hipMemcpy(gout, dout, sizeof gout, hipMemcpyDeviceToHost) ||
+        hipMemcpy(glse, dlse, sizeof glse, hipMemcpyDeviceToHost))
+      return 5;
+  }
   hipFree(dq); hipFree(dk); hipFree(dv); hipFree(dbt); hipFree(dlens); hipFree(dout);
   hipFree(dlse);
   if (dws) hipFree(dws);
