@@ -309,14 +309,17 @@ constexpr int kFillPerCu = 3;          // workgroups per CU the slot fill runs a
 constexpr int32_t kMinFillBlocks = 16;  // smallest task the slot fill makes (blocks)
 constexpr int32_t kMaxFillSplits = 8;  // nor splits a row into more tasks than this
 constexpr double kMaxFillRows = 0.8;   // mean row fill below which rows count as uneven
-constexpr double kMinFillSlots = 0.6;  // share of the slots a slot fill uses at least
+constexpr double kMinFillSlots = 0.65;  // expected tasks of a slot fill, as a share of the
+constexpr double kMaxFillSlots = 1.3;   // slots: at least / at most
 
 // The slot fill of the matrix-core kernel with one 16-head column group, for
 // rows of uneven length (mean fill of the table width known from the caller
-// and below 0.8): blocks per task such that one round of three workgroups per
-// CU holds every task, at least 60 % of those slots are used and no row
-// splits more than eight ways, or 0 when no task size does; the coarsest
-// such size wins. One workgroup of this kernel is a slow stream (its
+// and below 0.8): blocks per task such that the expected tasks make 65-130 %
+// of one round of three workgroups per CU and no row splits more than eight
+// ways, or 0 when no task size does; the coarsest such size wins. (Past one
+// round the few extra tasks are short ones: at 1.05-1.27 rounds split tasks
+// still beat the model's whole rows by 14-32 %, 8 / 1, 12 / 2 and 28 / 4
+// heads, batch 68-320.) One workgroup of this kernel is a slow stream (its
 // per-block chain: scores MFMAs, the cross-row max, the LDS round trip of V,
 // the P.V MFMAs), so uneven rows leave the CUs holding the longest ones
 // working long after the rest; three per CU, each with a share of the work,
@@ -336,7 +339,7 @@ int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots
     const int64_t S = (W + sb - 1) / sb;
     if (S > kMaxFillSplits) break;
     const double tasks = expected_tasks(n, kv_tasks, S, fill);
-    if (tasks > (double)slots) break;  // finer sizes only add tasks
+    if (tasks > kMaxFillSlots * (double)slots) break;  // finer sizes only add tasks
     if (tasks > kMinFillSlots * (double)slots) return sb;
   }
   return 0;
