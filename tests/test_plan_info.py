@@ -147,3 +147,25 @@ def test_token_total_steers_uneven_rows_to_the_slot_fill(gpu):
     # the workspace query covers any total
     need = ops.workspace_bytes(256, 8, 1, 128, 16, 256)
     assert need >= 256 * 8 * 4 * 128 * 4
+
+
+@pytest.mark.gpu
+def test_quarter_rows_just_past_one_row_per_cu(gpu):
+    """On the device: a little more than one (sequence, kv head) row per CU
+    (1.0-1.3) at D = 128 takes tasks of a quarter of the table width at three
+    workgroups per CU, on the matrix-core and the VALU kernel alike; one row
+    per CU, 1.4 rows per CU and D = 64 keep the model's whole rows."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    one = ops.decode_plan_info(cus, 8, 1, 128, 16, 256, torch.bfloat16)
+    assert one["split_blocks"] == 256 and one["wg_cap"] == 2
+    past = ops.decode_plan_info(cus + cus // 16, 8, 1, 128, 16, 256, torch.bfloat16)
+    assert past["kernel"] == "mm" and past["split_blocks"] == 64 and past["max_splits"] == 4
+    assert past["wg_cap"] in (0, 3)
+    narrow = ops.decode_plan_info(cus + cus // 16, 8, 1, 128, 16, 128, torch.bfloat16)
+    assert narrow["split_blocks"] == 32
+    mha = ops.decode_plan_info(cus // 32 + 1, 32, 32, 128, 16, 256, torch.float16)
+    assert mha["kernel"] == "valu" and mha["split_blocks"] == 64 and mha["wg_cap"] == 3
+    far = ops.decode_plan_info(cus * 14 // 10, 8, 1, 128, 16, 256, torch.bfloat16)
+    assert far["split_blocks"] == 256
+    d64 = ops.decode_plan_info((cus + cus // 16) // 2, 14, 2, 64, 16, 256, torch.bfloat16)
+    assert not (d64["split_blocks"] == 64 and d64["max_splits"] == 4 and d64["wg_cap"] in (0, 3))

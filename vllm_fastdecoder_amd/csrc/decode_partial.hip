@@ -345,6 +345,29 @@ int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots
   return 0;
 }
 
+// Quarter rows: a launch with a little more than one (sequence, kv head)
+// row per CU (1.0-1.3) on the 16-bit kernels at D = 128 cuts rows into
+// quarters of the table width (16+ blocks), whatever their lengths. With
+// whole rows the rows past one per CU land as second workgroups on CUs that
+// already stream one, and those CUs take about twice as long as the rest.
+// Measured on MI355X (bf16, HIP graph replay, three workgroups per CU):
+// 8 / 1 heads at 272 and 320 rows of 4096 tokens 136.4 / 139.9 us whole
+// against 104.2 / 113.6 us in quarters (rows of U[1024, 4096]: 87.0 / 92.8
+// -> 67.0 / 81.0 us; of 2048 tokens: 70.1 / 72.3 -> 54.7 / 61.4 us); MHA
+// (VALU kernel) at 288 and 320 rows of 4096 tokens 121.6 / 123.0 -> 100.2 /
+// 109.2 us, of U[1024, 4096] 76.7 / 76.8 -> 71.9 / 73.4 us. At exactly one
+// row per CU and from about 1.5 on, whole rows do as well or better; at
+// D = 64 the quarters lose on some length mixes, so the rule stays at D = 128.
+int32_t quarter_row_blocks(int32_t n, int32_t kv_tasks, int32_t D, bool f32, bool mfma,
+                           int cus, int32_t wt) {
+  const int64_t rows = (int64_t)n * kv_tasks;
+  if (f32 || mfma || D != 128 || cus <= 0 || wt < 4 * kMinFillBlocks) return 0;
+  if (rows <= cus || rows * 10 > (int64_t)cus * 13) return 0;
+  int32_t q = kMinFillBlocks;
+  while (q * 2 <= wt / 4) q *= 2;
+  return q;
+}
+
 }  // namespace
 
 // Blocks per task (16 .. 256) from a launch-time model. Only the shapes are
@@ -473,13 +496,22 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     sb = fill_split_blocks(n, kv_tasks, wt, (int64_t)kFillPerCu * cus, fill);
     filled = sb > 0;
   }
-  if (sb <= 0) sb = model_split_blocks(n, H, kv_tasks, D, kTileTokens, wt, elt);
+  bool quartered = false;
+  if (sb <= 0) {
+    sb = model_split_blocks(n, H, kv_tasks, D, kTileTokens, wt, elt);
+    const int32_t q = quarter_row_blocks(n, kv_tasks, D, f32, sp.mfma, cus, wt);
+    if (q > 0 && q < sb) {
+      sb = q;
+      quartered = true;
+    }
+  }
   sp.split_blocks = sb;
   sp.max_splits = wt > 0 ? (wt + sb - 1) / sb : 1;
-  // The slot fill runs at three workgroups per CU (a cap where the kernel
-  // would hold more; its own occupancy where that is three).
-  sp.wg_cap = filled ? (tiled_wgs_per_cu(sp, kv_dtype, D) > kFillPerCu ? kFillPerCu : 0)
-                     : sb >= 32 ? 2 : 0;
+  // The slot fill and quarter rows run at three workgroups per CU (a cap
+  // where the kernel would hold more; its own occupancy where that is three).
+  sp.wg_cap = filled || quartered
+                  ? (tiled_wgs_per_cu(sp, kv_dtype, D) > kFillPerCu ? kFillPerCu : 0)
+                  : sb >= 32 ? 2 : 0;
   const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=<k>: at most k per CU, 0 none (tuning)
   if (cap != nullptr && *cap != 0) sp.wg_cap = std::max(0, atoi(cap));
   return sp;
