@@ -169,3 +169,35 @@ def test_quarter_rows_just_past_one_row_per_cu(gpu):
     assert far["split_blocks"] == 256
     d64 = ops.decode_plan_info((cus + cus // 16) // 2, 14, 2, 64, 16, 256, torch.bfloat16)
     assert not (d64["split_blocks"] == 64 and d64["max_splits"] == 4 and d64["wg_cap"] in (0, 3))
+
+
+@pytest.mark.gpu
+def test_half_rows_for_full_rows_past_two_per_cu(gpu):
+    """On the device: 2.0-2.6 rows per CU at D = 128 take half-row tasks when
+    the token total shows the rows full (mean fill 0.8 or more); rows of
+    mixed length, or no total, keep whole rows."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    n = cus * 9 // 4
+    full = n * 256 * 16
+    whole = ops.decode_plan_info(n, 8, 1, 128, 16, 256, torch.bfloat16)
+    assert whole["split_blocks"] == 256
+    half = ops.decode_plan_info(n, 8, 1, 128, 16, 256, torch.bfloat16, total_tokens=full)
+    assert half["split_blocks"] == 128 and half["max_splits"] == 2
+    mixed = ops.decode_plan_info(n, 8, 1, 128, 16, 256, torch.bfloat16,
+                                 total_tokens=int(0.6 * full))
+    assert mixed["split_blocks"] == 256
+
+
+@pytest.mark.gpu
+def test_workspace_covers_every_total(gpu):
+    """The workspace query (which takes no total) covers what a total makes of
+    a plan: half rows on the VALU kernel for full MHA rows, the slot fill on
+    the matrix-core kernel for uneven ones."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for n, H, KVH, total_share, dt in ((cus * 17 // 256, 32, 32, 1.0, torch.float16),
+                                        (cus * 9 // 4, 8, 1, 1.0, torch.bfloat16),
+                                        (cus // 2, 8, 1, 0.6, torch.bfloat16)):
+        total = int(total_share * n * 256 * 16)
+        plan = ops.decode_plan_info(n, H, KVH, 128, 16, 256, dt, total_tokens=total)
+        need = n * H * plan["max_splits"] * (128 + 1) * 4 if plan["max_splits"] > 1 else 0
+        assert ops.workspace_bytes(n, H, KVH, 128, 16, 256) >= need, (n, H, KVH, plan)

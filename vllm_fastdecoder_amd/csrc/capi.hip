@@ -191,8 +191,8 @@ int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_
                                      dts[c], true, c == 0);
     most = std::max(most, decode_workspace_bytes(sp, n, num_heads, head_size));
     // what a token total may make of it (fd_paged_decode_partial_hint)
-    most = std::max(most, fill_workspace_bound(sp, n, num_heads, head_size, block_size,
-                                               bt_width));
+    most = std::max(most, fill_workspace_bound(sp, n, num_heads, num_kv_heads, head_size,
+                                               block_size, bt_width, dts[c]));
   }
   *bytes = most;
   return FD_OK;

@@ -316,10 +316,10 @@ constexpr double kMaxFillSlots = 1.3;   // slots: at least / at most
 // rows of uneven length (mean fill of the table width known from the caller
 // and below 0.8): blocks per task such that the expected tasks make 65-130 %
 // of one round of three workgroups per CU and no row splits more than eight
-// ways, or 0 when no task size does; the coarsest such size wins. (Past one
-// round the few extra tasks are short ones: at 1.05-1.27 rounds split tasks
-// still beat the model's whole rows by 14-32 %, 8 / 1, 12 / 2 and 28 / 4
-// heads, batch 68-320.) One workgroup of this kernel is a slow stream (its
+// ways, or 0 when no task size that splits rows does; the coarsest such size
+// wins. (Past one round the few extra tasks are short ones: at 1.05-1.27
+// rounds split tasks still beat the model's whole rows by 14-32 %, 8 / 1,
+// 12 / 2 and 28 / 4 heads, batch 68-320.) One workgroup of this kernel is a slow stream (its
 // per-block chain: scores MFMAs, the cross-row max, the LDS round trip of V,
 // the P.V MFMAs), so uneven rows leave the CUs holding the longest ones
 // working long after the rest; three per CU, each with a share of the work,
@@ -340,7 +340,9 @@ int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots
     if (S > kMaxFillSplits) break;
     const double tasks = expected_tasks(n, kv_tasks, S, fill);
     if (tasks > kMaxFillSlots * (double)slots) break;  // finer sizes only add tasks
-    if (tasks > kMinFillSlots * (double)slots) return sb;
+    // a fill splits rows; whole rows stay with the model and its cap (rows of
+    // mixed length at 2-2.6 per CU: -9 to -12 % without the cap)
+    if (S > 1 && tasks > kMinFillSlots * (double)slots) return sb;
   }
   return 0;
 }
@@ -358,13 +360,25 @@ int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots
 // 109.2 us, of U[1024, 4096] 76.7 / 76.8 -> 71.9 / 73.4 us. At exactly one
 // row per CU and from about 1.5 on, whole rows do as well or better; at
 // D = 64 the quarters lose on some length mixes, so the rule stays at D = 128.
+// Past two rows per CU (2.0-2.6) the same holds for rows of equal length
+// only: the two-per-CU cap then leaves a second round of whole rows, and
+// half rows gain (8 / 1 heads, 528-640 rows of 4096 tokens: 216.1 / 264.9 /
+// 278.0 -> 196.3 / 205.8 / 210.1 us; MHA on the VALU kernel +2 to +7 %),
+// while rows of mixed length balance by themselves and lose 3-11 % split.
+// So half rows need the caller's token total to show the rows full (mean
+// fill of the table 0.8 or more; fill = 0: unknown).
 int32_t quarter_row_blocks(int32_t n, int32_t kv_tasks, int32_t D, bool f32, bool mfma,
-                           int cus, int32_t wt) {
+                           int cus, int32_t wt, double fill) {
   const int64_t rows = (int64_t)n * kv_tasks;
   if (f32 || mfma || D != 128 || cus <= 0 || wt < 4 * kMinFillBlocks) return 0;
-  if (rows <= cus || rows * 10 > (int64_t)cus * 13) return 0;
+  int32_t parts = 0;
+  if (rows > cus && rows * 10 <= (int64_t)cus * 13)
+    parts = 4;
+  else if (fill >= kMaxFillRows && rows > 2 * (int64_t)cus && rows * 10 <= (int64_t)cus * 26)
+    parts = 2;
+  if (parts == 0) return 0;
   int32_t q = kMinFillBlocks;
-  while (q * 2 <= wt / 4) q *= 2;
+  while (q * 2 <= wt / parts) q *= 2;
   return q;
 }
 
@@ -491,15 +505,18 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   const int32_t kv_tasks = KVH * sp.passes;
   const int elt = f32 ? 4 : 2;
   bool filled = false;
-  if (sb <= 0 && fill > 0.0 && fill < kMaxFillRows && sp.mm && sp.kernel_g == 16 && cus > 0) {
-    // uneven rows on the one-column-group matrix-core kernel: the slot fill
+  if (sb <= 0 && fill > 0.0 && fill < kMaxFillRows && sp.mm && sp.kernel_g == 16 && cus > 0 &&
+      2 * (int64_t)n * kv_tasks <= 3 * (int64_t)cus) {
+    // uneven rows on the one-column-group matrix-core kernel, up to 1.5 rows
+    // per CU (with more, they balance by themselves: -3 to -6 % split at two
+    // rows per CU, rows of 2048 tokens): the slot fill
     sb = fill_split_blocks(n, kv_tasks, wt, (int64_t)kFillPerCu * cus, fill);
     filled = sb > 0;
   }
   bool quartered = false;
   if (sb <= 0) {
     sb = model_split_blocks(n, H, kv_tasks, D, kTileTokens, wt, elt);
-    const int32_t q = quarter_row_blocks(n, kv_tasks, D, f32, sp.mfma, cus, wt);
+    const int32_t q = quarter_row_blocks(n, kv_tasks, D, f32, sp.mfma, cus, wt, fill);
     if (q > 0 && q < sb) {
       sb = q;
       quartered = true;
@@ -517,13 +534,23 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   return sp;
 }
 
-size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t D, int32_t BS,
-                            int32_t bt_width) {
-  if (!sp.fast || !sp.mm || sp.kernel_g != 16 || BS % kTileTokens != 0 || bt_width <= 0) return 0;
-  const int64_t wt = (int64_t)bt_width * (BS / kTileTokens);
+size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t KVH, int32_t D,
+                            int32_t BS, int32_t bt_width, int32_t kv_dtype) {
+  const int cus = device_cus();
+  if (!sp.fast || cus <= 0 || BS % kTileTokens != 0 || bt_width <= 0) return 0;
+  const int64_t wt64 = (int64_t)bt_width * (BS / kTileTokens);
+  const int32_t wt = (int32_t)std::min<int64_t>(wt64, INT32_MAX);
+  int64_t most = 0;
+  // the slot fill: at most kMaxFillSplits tasks per row
+  if (sp.mm && sp.kernel_g == 16)
+    most = std::min<int64_t>(kMaxFillSplits, (wt64 + kMinFillBlocks - 1) / kMinFillBlocks);
+  // half rows for full rows (quarter_row_blocks given a total)
+  const int32_t half = quarter_row_blocks(n, KVH * sp.passes, D, kv_dtype == FD_F32, sp.mfma, cus,
+                                          wt, 1.0);
+  if (half > 0) most = std::max<int64_t>(most, (wt64 + half - 1) / half);
+  if (most <= 1) return 0;
   SplitPlan b = sp;
-  b.max_splits =
-      (int32_t)std::min<int64_t>(kMaxFillSplits, (wt + kMinFillBlocks - 1) / kMinFillBlocks);
+  b.max_splits = (int32_t)most;
   return decode_workspace_bytes(b, n, H, D);
 }
 

@@ -226,10 +226,10 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
                       double fill = 0.0);
 size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H,
                               int32_t D);
-// Workspace the slot fill may need for a plan of these sizes whatever the
-// rows' token total (0 when the fill cannot apply to it).
-size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t D, int32_t BS,
-                            int32_t bt_width);
+// Workspace a plan of these sizes may need whatever the rows' token total
+// (the slot fill, half rows), 0 when neither can apply to it.
+size_t fill_workspace_bound(const SplitPlan& sp, int32_t n, int32_t H, int32_t KVH, int32_t D,
+                            int32_t BS, int32_t bt_width, int32_t kv_dtype);
 int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s);
 
 struct MergeArgs {
