@@ -209,30 +209,33 @@ def test_random_shape_with_token_total_matches_oracle(gpu, i):
 
 
 def _split_case(name, cus):
-    """(n, H, KVH, dtype, full rows, hinted, expected split_blocks) of the
-    planner's row-splitting rules at 64-block tables of 16 tokens, D = 128."""
+    """(n, H, KVH, D, dtype, full rows, hinted, expected split_blocks) of the
+    planner's row-splitting rules at 64-block tables of 16 tokens."""
     return {
         # 2.25 full rows per CU, total given: half rows (32 of 64 blocks)
-        "half_rows": (cus * 9 // 4, 4, 1, torch.bfloat16, True, True, 32),
+        "half_rows": (cus * 9 // 4, 4, 1, 128, torch.bfloat16, True, True, 32),
+        # the same at D = 64, whose rules need all but equal rows
+        "half_rows_d64": (cus * 9 // 8, 14, 2, 64, torch.bfloat16, True, True, 32),
+        "quarter_rows_d64": (cus * 5 // 8, 14, 2, 64, torch.float16, True, True, 16),
         # 1.06 rows per CU, no total: quarter rows on the matrix-core kernel
-        "quarter_rows_mm": (cus + cus // 16, 4, 1, torch.bfloat16, False, False, 16),
+        "quarter_rows_mm": (cus + cus // 16, 4, 1, 128, torch.bfloat16, False, False, 16),
         # 1.1 MHA rows per CU: quarter rows on the VALU kernel
-        "quarter_rows_valu": (cus // 32 + 1, 32, 32, torch.float16, False, False, 16),
+        "quarter_rows_valu": (cus // 32 + 1, 32, 32, 128, torch.float16, False, False, 16),
         # one row per CU of mixed length, total given: the slot fill
-        "slot_fill": (cus, 4, 1, torch.bfloat16, False, True, 16),
+        "slot_fill": (cus, 4, 1, 128, torch.bfloat16, False, True, 16),
     }[name]
 
 
-@pytest.mark.parametrize("name", ["half_rows", "quarter_rows_mm", "quarter_rows_valu",
-                                  "slot_fill"])
+@pytest.mark.parametrize("name", ["half_rows", "half_rows_d64", "quarter_rows_d64",
+                                  "quarter_rows_mm", "quarter_rows_valu", "slot_fill"])
 def test_row_splitting_plans_match_oracle(gpu, name):
     """The launches whose rows the planner cuts by row count and fill (half
     rows, quarter rows, the slot fill) at the row counts that trigger them on
     this device, run through paged_decode in vLLM's layout, with the plan
     asserted and the output checked against the oracle (fp32 out, 2e-3)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
-    n, H, KVH, dtype, full, hinted, want_sb = _split_case(name, cus)
-    D, BS, W = 128, 16, 64
+    n, H, KVH, D, dtype, full, hinted, want_sb = _split_case(name, cus)
+    BS, W = 16, 64
     C = n * W + 2
     q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, dtype, max_len=W * BS, seed=77)
     if full:
@@ -249,7 +252,7 @@ def test_row_splitting_plans_match_oracle(gpu, name):
         pos += nb
     total = int(lens.sum()) if hinted else None
     info = ops.decode_plan_info(n, H, KVH, D, BS, W, dtype, total_tokens=total)
-    what = f"{name}: n={n} H={H} KVH={KVH} {dtype} total={total} plan={info}"
+    what = f"{name}: n={n} H={H} KVH={KVH} D={D} {dtype} total={total} plan={info}"
     print(what, flush=True)
     assert info["split_blocks"] == want_sb and info["max_splits"] == W // want_sb, what
     scale = 1.0 / math.sqrt(D)

@@ -201,3 +201,20 @@ def test_workspace_covers_every_total(gpu):
         plan = ops.decode_plan_info(n, H, KVH, 128, 16, 256, dt, total_tokens=total)
         need = n * H * plan["max_splits"] * (128 + 1) * 4 if plan["max_splits"] > 1 else 0
         assert ops.workspace_bytes(n, H, KVH, 128, 16, 256) >= need, (n, H, KVH, plan)
+
+
+@pytest.mark.gpu
+def test_d64_rows_split_only_when_the_total_shows_them_full(gpu):
+    """On the device at D = 64: 1.25 and 2.25 (sequence, kv head) rows per CU
+    take quarter and half rows when the token total shows the rows all but
+    full (mean fill 0.95 or more); a mean fill of 0.85, or no total, keeps
+    the model's plan."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    for n, sb, splits in ((cus * 5 // 8, 64, 4), (cus * 9 // 8, 128, 2)):
+        full = n * 256 * 16
+        base = ops.decode_plan_info(n, 14, 2, 64, 16, 256, torch.bfloat16)
+        split = ops.decode_plan_info(n, 14, 2, 64, 16, 256, torch.bfloat16, total_tokens=full)
+        assert split["split_blocks"] == sb and split["max_splits"] == splits, (n, split)
+        mixed = ops.decode_plan_info(n, 14, 2, 64, 16, 256, torch.bfloat16,
+                                     total_tokens=int(0.85 * full))
+        assert mixed == base, (n, mixed, base)
