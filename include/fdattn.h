@@ -197,6 +197,9 @@ typedef struct {
   int32_t max_splits;     /* tasks per row at most (> 1: a combine pass) */
   int32_t wg_cap;         /* workgroups per compute unit the launch allows at most
                              (0: the kernel's own occupancy) */
+  int32_t wave_blocks;    /* > 0: a task's four waves work only as far as its range
+                             holds this many 16-token tiles each (a shorter range
+                             works with fewer waves); 0: every wave works */
 } FdDecodePlan;
 
 int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,

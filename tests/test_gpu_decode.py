@@ -255,6 +255,43 @@ def test_full_size_workloads_match_oracle(gpu, name):
     assert_lse_close(l, ref_lse)
 
 
+@pytest.mark.parametrize("wave_blocks", [None, "0", "1", "5", "16", "300"])
+@pytest.mark.parametrize("layout", ["vllm", "host"])
+def test_working_waves_by_row_length_match_oracle(gpu, wave_blocks, layout, monkeypatch):
+    """The small-batch workload (n=8, 32/32, D=128, fp16, rows of U[128,
+    1024] tokens: one task per CU) with the tasks' working waves set by row
+    length: None = the planner's choice (16 tiles per wave at this table
+    width, so rows of 1-16 tiles take one wave, 17-32 two ...), "0" = every
+    wave works, and other tile counts per wave, including 1 (four waves for
+    every row of 4+ tiles) and 300 (one wave unless a wave's 64 block ids
+    would not hold the row). fp32 out against the float64 oracle."""
+    if wave_blocks is None:
+        monkeypatch.delenv("FD_WAVE_BLOCKS", raising=False)
+    else:
+        monkeypatch.setenv("FD_WAVE_BLOCKS", wave_blocks)
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    q = cases.queries(w, gpu)
+    out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+    if layout == "vllm":
+        kc, vc, kv = cases.kv_pool(w, pool, "vllm", gpu)
+        o, l = ops.paged_decode(q, kc, vc, bt.to(gpu), lens.to(gpu), w.scale, out=out)
+        torch.cuda.synchronize()
+        kv_cpu = kv.cpu()
+        ref_out, ref_lse, st = oracle.decode_attn_f64(q, kv_cpu[..., : w.D], kv_cpu[..., w.D :],
+                                                      oracle.VLLM_DIMS, bt, lens, w.scale)
+        assert st == 0
+    else:
+        k, v, _ = cases.kv_pool(w, pool, "host", "cpu")
+        o, l = run_host_layout(q.cpu(), k, v, bt, lens, w.scale, torch.float32, gpu)
+        ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q.cpu(), k, v, bt, lens, w.scale)
+    assert_out_close(o, ref_out, 2e-3)
+    assert_lse_close(l, ref_lse)
+    if wave_blocks is None:
+        plan = ops.decode_plan_info(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1], w.dtype)
+        assert plan["kernel"] == "valu" and plan["wave_blocks"] == 16, plan
+
+
 GQA_LENS = [0, 1, 15, 16, 17, 93, 160, 47]
 
 

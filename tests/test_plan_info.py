@@ -20,6 +20,7 @@ def plan(n, H, KVH, D, W, dtype=BF16, BS=16, **kw):
 def _no_overrides(monkeypatch):
     monkeypatch.delenv("FD_DECODE_KERNEL", raising=False)
     monkeypatch.delenv("FD_SPLIT_BLOCKS", raising=False)
+    monkeypatch.delenv("FD_WAVE_BLOCKS", raising=False)
 
 
 @pytest.mark.parametrize("H,KVH,D,kernel,slots,passes", [
@@ -169,6 +170,32 @@ def test_quarter_rows_just_past_one_row_per_cu(gpu):
     assert far["split_blocks"] == 256
     d64 = ops.decode_plan_info((cus + cus // 16) // 2, 14, 2, 64, 16, 256, torch.bfloat16)
     assert not (d64["split_blocks"] == 64 and d64["max_splits"] == 4 and d64["wg_cap"] in (0, 3))
+
+
+@pytest.mark.gpu
+def test_working_waves_by_row_length_on_small_launches(gpu):
+    """On the device: launches of at most one task per CU on the VALU kernel at
+    D = 128 give each task's waves a quarter of the longest task's tiles
+    (table width, or the task size when rows split); one task more than the
+    CUs, another kernel or another head size keeps every wave working."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    at = ops.decode_plan_info(cus // 32, 32, 32, 128, 16, 64, torch.float16)
+    assert at["kernel"] == "valu" and at["max_splits"] == 1 and at["wave_blocks"] == 16, at
+    g2 = ops.decode_plan_info(cus // 16, 32, 16, 128, 16, 50, torch.bfloat16)
+    assert g2["kernel"] == "valu" and g2["wave_blocks"] == 13, g2
+    big_bs = ops.decode_plan_info(cus // 32, 32, 32, 128, 32, 64, torch.float16)
+    if big_bs["max_splits"] == 1:
+        assert big_bs["wave_blocks"] == 32, big_bs  # 128 tiles of 16 tokens
+    over = ops.decode_plan_info(cus // 32 + 1, 32, 32, 128, 16, 64, torch.float16)
+    assert over["wave_blocks"] == 0, over
+    for other in (ops.decode_plan_info(cus // 32, 32, 32, 64, 16, 64, torch.float16),
+                  ops.decode_plan_info(cus // 32, 32, 8, 128, 16, 64, torch.bfloat16),
+                  ops.decode_plan_info(cus // 32, 32, 32, 128, 16, 64, torch.float32)):
+        assert other["wave_blocks"] == 0, other
+    # batch 1 with rows longer than one task: the task size sets the tiles per wave
+    split = ops.decode_plan_info(1, 32, 32, 128, 16, 1024, torch.float16)
+    if split["max_splits"] * 32 <= cus:
+        assert split["wave_blocks"] == (min(split["split_blocks"], 1024) + 3) // 4, split
 
 
 @pytest.mark.gpu

@@ -171,7 +171,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 8; }
+int fd_abi_version(void) { return 9; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -225,6 +225,7 @@ int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int3
   plan->split_blocks = sp.split_blocks;
   plan->max_splits = sp.max_splits;
   plan->wg_cap = sp.fast ? sp.wg_cap : 0;
+  plan->wave_blocks = sp.fast ? sp.wave_blocks : 0;
   return FD_OK;
 }
 

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_f32_kernel(Tiled
   // Reduces the resident half block u (in `slot`); fewer than 8 valid tokens
   // only in a tier's last block.
   auto compute_half = [&](int slot, int u) {
-    const int ntok = block_tokens<TWO>(t, wb.first + kWavesPerTask * (u >> 1)) - HALF * (u & 1);
+    const int ntok = block_tokens<TWO>(t, wb.first + wb.stride * (u >> 1)) - HALF * (u & 1);
     if (ntok <= 0) return;  // the empty second half of a short last block
     float s[G][STEPS];
 #pragma unroll

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
   const WaveBlocks wb = wave_blocks<TWO>(p, t, wave, lane);
   const int nw = wb.nw;
   auto ntok_of = [&](int k) -> int {
-    return block_tokens<TWO>(t, wb.first + kWavesPerTask * k);
+    return block_tokens<TWO>(t, wb.first + wb.stride * k);
   };
 
   // K is single-buffered (its registers are free once the block's matrix-core
@@ -252,12 +252,9 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
   // head hg's running max; each row's sum and V slices are scaled by
   // exp2(m_row - M) and summed over the rows (and, for D = 64, over the two
   // token halves of a row).
-  float M = fmaxf(m, shfl_xor_f32(m, 16));
-  M = fmaxf(M, shfl_xor_f32(M, 32));
+  const float M = xor_max<16>(m);
   const float Ms = M == neg_inf() ? 0.f : M;
-  float lt = l * fast_exp2(m - Ms);  // 0 for a row that saw no token
-  lt += shfl_xor_f32(lt, 16);
-  lt += shfl_xor_f32(lt, 32);
+  const float lt = xor_sum<16>(l * fast_exp2(m - Ms));  // 0 for a row that saw no token
   static_for<0, G>([&](auto gc) {
     constexpr int g = decltype(gc)::value;
     const float w = fast_exp2(row_bcast<g>(m) - row_bcast<g>(Ms));
@@ -267,10 +264,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mfma_kernel(Tile
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = acc[g][h][e] * w;
 #pragma unroll
-      for (int x = VM::LPS; x < kWave; x <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += shfl_xor_f32(o[e], x);
-      }
+      for (int e = 0; e < 8; ++e) o[e] = xor_sum<VM::LPS>(o[e]);
       if (lane < VM::LPS) {
         float4* dst = reinterpret_cast<float4*>(&ws.acc[wave][g][(vchunk + 16 * h) * 8]);
         dst[0] = make_float4(o[0], o[1], o[2], o[3]);

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
   const WaveBlocks wb = wave_blocks<TWO>(p, t, wave, lane);
   const int nw = wb.nw;
   auto ntok_of = [&](int k) -> int {
-    return block_tokens<TWO>(t, wb.first + kWavesPerTask * k);
+    return block_tokens<TWO>(t, wb.first + wb.stride * k);
   };
 
   // K and V double-buffered in registers: block k+1's loads are issued right
@@ -268,8 +268,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
 #pragma unroll
     for (int g = 0; g < CG; ++g) {
       float bmax = fmaxf(fmaxf(s[g][0], s[g][1]), fmaxf(s[g][2], s[g][3]));
-      bmax = fmaxf(bmax, shfl_xor_f32(bmax, 16));
-      bmax = fmaxf(bmax, shfl_xor_f32(bmax, 32));
+      bmax = xor_max<16>(bmax);
       const bool raise = bmax > m[g] + kLazyRescale;  // false while both are -inf
       if (__ballot(raise) != 0) {
         const float mn = raise ? bmax : m[g];
@@ -344,8 +343,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_mm_kernel(TiledP
   const bool write_final = t.nsplit == 1;
 #pragma unroll
   for (int g = 0; g < CG; ++g) {
-    float lt = l[g] + shfl_xor_f32(l[g], 16);
-    lt += shfl_xor_f32(lt, 32);
+    const float lt = xor_sum<16>(l[g]);
     __syncthreads();  // the V staging (g = 0) or the previous group's merge is done
 #pragma unroll
     for (int c = 0; c < NC; ++c) {

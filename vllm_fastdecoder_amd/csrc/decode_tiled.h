@@ -80,6 +80,7 @@ struct TiledParams {
   float* part_lse;  // [n, H, S] fp32 (natural-log LSE of each partial)
   int32_t S;        // max splits per (sequence, kv head)
   int32_t split_blocks;
+  int32_t wave_blocks;  // blocks per working wave (0: every wave works; wave_blocks())
   bool xcd_group;   // adjacent kv heads of a row on one XCD (xcd_task)
 };
 
@@ -330,13 +331,15 @@ __device__ __forceinline__ void write_empty(const TiledParams& p, const Task& t,
   }
 }
 
-// A wave's blocks of its task are b_begin + wave + 4k. Their ids are read
+// A wave's blocks of its task are b_begin + wave + s k, s = the task's
+// working waves (4 unless p.wave_blocks says fewer). Their ids are read
 // once, one per lane (at most 64), range-checked together against their
 // tier's cache and later picked with v_readlane; a bad id is replaced by 0
 // (every read stays inside the cache) and flags the row. The wave's blocks
 // from index k1 on are in tier 1.
 struct WaveBlocks {
   int first;   // the wave's first block index in the row
+  int stride;  // block index step between the wave's blocks (the task's working waves)
   int nw;      // blocks of this wave
   int k1;      // first of the wave's blocks in tier 1 (>= nw: none)
   int my_bid;  // lane k: id of the cache block holding the wave's k-th tile
@@ -344,19 +347,31 @@ struct WaveBlocks {
   bool bad;
 };
 
+// With p.wave_blocks > 0 a task works with as many of its waves as give
+// each about that many blocks (at least one, at most four); the rest only
+// take part in the merge. A short row then keeps fewer blocks in flight than
+// a long one.
 template <bool TWO>
 __device__ __forceinline__ WaveBlocks wave_blocks(const TiledParams& p, const Task& t, int wave,
                                                   int lane) {
   WaveBlocks w;
+  int ws = kWavesPerTask;
+  if (p.wave_blocks > 0) {
+    // (each wave's block ids fit its 64 lanes: nblk <= split_blocks <= 256)
+    const int nblk = t.b_end - t.b_begin;
+    ws = max((nblk + p.wave_blocks - 1) / p.wave_blocks,
+             (nblk + kMaxWaveBlocks - 1) / kMaxWaveBlocks);
+    ws = min(kWavesPerTask, max(1, ws));
+  }
+  w.stride = ws;
   w.first = t.b_begin + wave;
-  w.nw = w.first < t.b_end ? (t.b_end - w.first + kWavesPerTask - 1) / kWavesPerTask : 0;
-  w.k1 = TWO ? (t.nba > w.first ? (t.nba - w.first + kWavesPerTask - 1) / kWavesPerTask : 0)
-             : w.nw;
+  w.nw = wave < ws && w.first < t.b_end ? (t.b_end - w.first + ws - 1) / ws : 0;
+  w.k1 = TWO ? (t.nba > w.first ? (t.nba - w.first + ws - 1) / ws : 0) : w.nw;
   int bid = 0, sub = 0;
   bool my_bad = false;
   if (lane < w.nw) {
     // tile u of the row: tile u % tpb of the row's cache block u / tpb
-    const int u = w.first + kWavesPerTask * lane;
+    const int u = w.first + ws * lane;
     if (TWO && u >= t.nba) {
       const TierParams& tp = p.tier[1];
       const int ut = u - t.nba;
@@ -398,19 +413,17 @@ __device__ __forceinline__ void publish_wave_state(WaveStates<D, G>& ws, int wav
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float M = m[g];
-#pragma unroll
-    for (int x = LPT; x < kWave; x <<= 1) M = fmaxf(M, shfl_xor_f32(M, x));
+    if constexpr (LPT < kWave) M = xor_max<LPT>(M);
     const float Ms = M == neg_inf() ? 0.f : M;
     const float w = fast_exp2(m[g] - Ms);
     float lt = l[g] * w;
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = acc[g][e] * w;
+    if constexpr (LPT < kWave) {
+      lt = xor_sum<LPT>(lt);
 #pragma unroll
-    for (int x = LPT; x < kWave; x <<= 1) {
-      lt += shfl_xor_f32(lt, x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += shfl_xor_f32(o[e], x);
+      for (int e = 0; e < 8; ++e) o[e] = xor_sum<LPT>(o[e]);
     }
     if (lane < LPT) {
       float4* dst = reinterpret_cast<float4*>(&ws.acc[wave][g][chunk * 8]);

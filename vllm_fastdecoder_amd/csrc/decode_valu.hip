@@ -124,7 +124,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   // Reduces the wave's resident block k (in `slot`); fewer than 16 valid
   // tokens only in a tier's last block.
   auto compute_block = [&](int slot, int k) {
-    const int ntok = block_tokens<TWO>(t, wb.first + kWavesPerTask * k);
+    const int ntok = block_tokens<TWO>(t, wb.first + wb.stride * k);
     if constexpr (ADJ) {
       if (adj_block(k)) {
 #pragma unroll

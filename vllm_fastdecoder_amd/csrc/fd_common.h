@@ -147,6 +147,56 @@ __device__ __forceinline__ float shfl_xor_f32(float x, int mask) {
   return __shfl_xor(x, mask, kWave);
 }
 
+// x and the value of the lane at lane ^ kMask (kMask = 8, 16 or 32) as the
+// pair (a, b), in an order that depends on the lane: a commutative op of the
+// two is op(x, partner) on every lane. VALU only, no LDS round trip (a
+// __shfl_xor is a ds_bpermute): kMask = 8 is a DPP row rotate by 8 (the xor-8
+// partner inside a 16-lane row); 16 and 32 are gfx950's v_permlane16_swap /
+// v_permlane32_swap with x as both operands, which leave [x0, x0, x2, x2]
+// and [x1, x1, x3, x3] (16-lane rows), or [lo, lo] and [hi, hi] (32-lane
+// halves).
+constexpr int kDppRowRor8 = 0x128;  // lane i <- lane (i + 8) % 16 in each 16
+
+template <int kMask>
+__device__ __forceinline__ void xor_pair(float x, float& a, float& b) {
+  static_assert(kMask == 8 || kMask == 16 || kMask == 32, "xor_pair: unsupported mask");
+  if constexpr (kMask == 8) {
+    a = x;
+    b = dpp<kDppRowRor8>(x);
+  } else {
+    const uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if constexpr (kMask == 16) {
+      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      a = __builtin_bit_cast(float, (uint32_t)r[0]);
+      b = __builtin_bit_cast(float, (uint32_t)r[1]);
+    } else {
+      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      a = __builtin_bit_cast(float, (uint32_t)r[0]);
+      b = __builtin_bit_cast(float, (uint32_t)r[1]);
+    }
+  }
+}
+
+// Sum / max over the lanes that differ from this one in the bits kFrom,
+// 2 kFrom, .. 32 of the lane index (kFrom = 8, 16 or 32): every lane of such
+// a group receives the group's result.
+template <int kFrom>
+__device__ __forceinline__ float xor_sum(float x) {
+  float a, b;
+  xor_pair<kFrom>(x, a, b);
+  x = a + b;
+  if constexpr (kFrom < 32) x = xor_sum<2 * kFrom>(x);
+  return x;
+}
+template <int kFrom>
+__device__ __forceinline__ float xor_max(float x) {
+  float a, b;
+  xor_pair<kFrom>(x, a, b);
+  x = fmaxf(a, b);
+  if constexpr (kFrom < 32) x = xor_max<2 * kFrom>(x);
+  return x;
+}
+
 __device__ __forceinline__ float wave_sum(float x) {
   for (int m = 32; m >= 1; m >>= 1) x += shfl_xor_f32(x, m);
   return x;
@@ -213,6 +263,7 @@ struct SplitPlan {
   int32_t kernel_d;      // head size the tiled kernel is built for: 64, 128 or 256
   int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
                          // kernel_g), each over the same blocks
+  int32_t wave_blocks;   // blocks per working wave of a task (0: every wave works)
   int* occupancy_query;  // planner only: when set, the tiled launchers store the selected
                          // kernel's workgroups per CU there instead of launching it
 };

@@ -127,9 +127,10 @@ def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtyp
     how it is cut into tasks (fd_decode_plan_info): {"kernel": "valu" | "mm" |
     "mfma" | "f32" | "generic", "heads_per_task", "passes", "split_blocks",
     "max_splits", "wg_cap" (workgroups per CU the launch allows, 0 = the
-    kernel's own occupancy), "capped" (wg_cap > 0)}. total_tokens: the rows'
-    token total a paged_decode call is given (None: unknown). Honours
-    FD_DECODE_KERNEL / FD_SPLIT_BLOCKS / FD_WG_CAP."""
+    kernel's own occupancy), "capped" (wg_cap > 0), "wave_blocks" (tiles per
+    working wave, 0 = every wave works)}. total_tokens: the rows' token total
+    a paged_decode call is given (None: unknown). Honours FD_DECODE_KERNEL /
+    FD_SPLIT_BLOCKS / FD_WG_CAP / FD_WAVE_BLOCKS."""
     plan = _lib.FdDecodePlan()
     _lib.check(_lib.load_lib().fd_decode_plan_info(n, H, KVH, D, BS, width, _DT[dtype],
                                                    int(aligned), int(host_tier),
@@ -137,7 +138,8 @@ def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtyp
                                                    ctypes.byref(plan)))
     return {"kernel": _lib.FD_KERNEL_NAMES[plan.kernel], "heads_per_task": plan.heads_per_task,
             "passes": plan.passes, "split_blocks": plan.split_blocks,
-            "max_splits": plan.max_splits, "wg_cap": plan.wg_cap, "capped": plan.wg_cap > 0}
+            "max_splits": plan.max_splits, "wg_cap": plan.wg_cap, "capped": plan.wg_cap > 0,
+            "wave_blocks": plan.wave_blocks}
 
 
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
