@@ -498,6 +498,7 @@ class DecodeLeg:
         note = (f"one HIP graph of {steps} launches over {self.copies} pool copies, HIP events "
                 f"around {replays} replays after {warmup} eager warm-ups{warm}")
         del g
+        ops.release_workspace(side)
         return ms, self.nbytes, self.kvb, self.lens, note
 
     def release(self):

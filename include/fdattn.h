@@ -136,15 +136,22 @@ int fd_paged_decode_partial(
 
 /* fd_paged_decode_partial for a caller that knows the rows' token total
  * (the sum of lens over the n rows; a serving step's scheduler has it on the
- * host). Results are those of fd_paged_decode_partial; only the task sizes
- * may differ. The launch plan otherwise sees only the table width, and rows
- * of uneven length (mean fill of bt_width * block_size below 0.8) on the
- * matrix-core kernel with 16 heads per task are then cut into tasks that
- * fill three workgroups per CU, where rows of equal length keep whole-row
- * tasks. total_tokens = 0: unknown (the same plan as
- * fd_paged_decode_partial); a wrong total costs time, never correctness.
- * No counterpart in the reference: its FlashAttention call plans from
- * max_seqlen_k alone (fastdecode/backend.py:306-314). */
+ * host). The launch plan otherwise sees only the table width; the total
+ * gives the rows' mean fill of bt_width * block_size, which selects three
+ * plans that cut rows into more tasks:
+ *   - rows of uneven length (fill below 0.8) on the matrix-core kernel with
+ *     16 heads per task, at up to 1.5 rows per CU: tasks that fill three
+ *     workgroups per CU ("slot fill");
+ *   - full rows (fill 0.8 or more) at 2.0-2.6 (sequence, kv head) rows per
+ *     CU and D = 128: half-row tasks;
+ *   - all but equal rows (fill 0.95 or more) at D = 64: quarter-row tasks at
+ *     1.0-1.3 rows per CU and half rows at 2.0-2.6.
+ * Results agree with fd_paged_decode_partial's within rounding: a different
+ * task split sums the fp32 partials in a different order, so hinted and
+ * unhinted calls are not bit-identical. total_tokens = 0: unknown (the same
+ * plan as fd_paged_decode_partial); a wrong total costs time, never
+ * correctness. No counterpart in the reference: its FlashAttention call
+ * plans from max_seqlen_k alone (fastdecode/backend.py:306-314). */
 int fd_paged_decode_partial_hint(
     const void* q, int64_t q_stride_seq, int64_t q_stride_head,
     const void* k_cache, const void* v_cache,
@@ -213,8 +220,11 @@ int fd_decode_plan_info(int32_t n, int32_t num_heads, int32_t num_kv_heads, int3
  * cannot allocate device memory (code under HIP graph capture, serving loops
  * that forbid hipMalloc). No counterpart in the reference. Same arguments,
  * kernels and results as fd_paged_decode_partial; the split workspace is a
- * fixed array of FD_NOALLOC_SCRATCH_BYTES in each GPU's memory, held from
- * the first call on that GPU until the process ends. Sizes whose workspace
+ * file-scope device array of FD_NOALLOC_SCRATCH_BYTES (32 MiB). Each GPU on
+ * which the library's device code is loaded holds one such array until the
+ * process ends, whether or not this entry point is ever called: every
+ * process that runs the library's kernels on a GPU pays 32 MiB of its
+ * memory for it. Sizes whose workspace
  * (fd_paged_decode_workspace_size) exceeds it are rejected with
  * FD_ERR_WORKSPACE before anything is written. The call allocates nothing.
  * Calls that may overlap on one GPU (other streams or threads) share the
@@ -400,9 +410,14 @@ int fd_check_slots(const int64_t* slots, int64_t m, int64_t capacity,
  * directly over the link with no staging copy.
  * ------------------------------------------------------------------------ */
 int fd_host_alloc(size_t bytes, void** host_ptr);
-/* Waits for the work enqueued on every device, then frees the block. If a
- * wait fails (a stream capture under way, say) the block is kept and the
- * call returns FD_ERR_HIP: call it outside capture. */
+/* Frees a block made by fd_host_alloc (NULL: no-op; any other pointer is
+ * FD_ERR_INVALID). It first waits for the work enqueued on the device that
+ * was current at fd_host_alloc (hipDeviceSynchronize on that device only;
+ * no other device is touched), so kernels still reading or writing the
+ * block over the link finish before it goes; a caller that also uses the
+ * block from other devices synchronises those first. Not to be called
+ * during a stream capture: the wait then fails, the block is kept and the
+ * call returns FD_ERR_HIP with "block kept" in fd_last_error(). */
 int fd_host_free(void* host_ptr);
 /* Device address of a pinned allocation made by fd_host_alloc. */
 int fd_host_device_pointer(void* host_ptr, void** device_ptr);

@@ -222,6 +222,17 @@ def test_host_entry_points_reject_bad_arguments():
     assert lib.fd_host_set_threads(0) == _lib.FD_OK
 
 
+def test_host_free_takes_only_its_own_blocks():
+    """fd_host_free: NULL is a no-op; a pointer fd_host_alloc did not make is
+    rejected with FD_ERR_INVALID before any device is waited for or touched
+    (the block registry is checked first; no GPU needed)."""
+    lib = _lib.load_lib()
+    assert lib.fd_host_free(None) == _lib.FD_OK
+    buf = (ctypes.c_uint8 * 64)()
+    assert lib.fd_host_free(ctypes.cast(buf, ctypes.c_void_p)) == _lib.FD_ERR_INVALID
+    assert b"not allocated by fd_host_alloc" in lib.fd_last_error()
+
+
 def test_missing_library_raises_instead_of_falling_back(monkeypatch, tmp_path):
     """Without the built library every entry point raises: there is no
     CPU or PyTorch path behind the kernels."""

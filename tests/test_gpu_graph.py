@@ -27,7 +27,7 @@ def _replays(gpu, q, step, outs, n_replays=4, ws_bytes=0):
     torch.cuda.synchronize()
     side = torch.cuda.Stream(device=gpu)
     ops.reserve_workspace(side, ws_bytes)
-    before = dict(ops.WORKSPACE._bufs)
+    before = {k: v for k, v in ops.WORKSPACE._bufs.items()}
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=side):
         step()
@@ -48,6 +48,8 @@ def _replays(gpu, q, step, outs, n_replays=4, ws_bytes=0):
         for a, b in zip(got, outs):
             assert torch.equal(a, b), f"replay {r} differs from the eager call"
     assert torch.isfinite(x).all()
+    del g
+    ops.release_workspace(side)
 
 
 @pytest.mark.parametrize("split", ["0", "2"])
@@ -110,3 +112,74 @@ def test_fused_split_in_a_graph(gpu):
 
     _replays(gpu, q, step, [out, lse],
              ws_bytes=ops.workspace_bytes(n, H, 32, D, 16, bt_g.shape[1] + bt_c.shape[1]))
+
+
+def test_reserved_workspace_outlives_growth_and_eviction(gpu, monkeypatch):
+    """A graph captured with a reserved workspace keeps its buffer's address.
+    After capture, a larger eager call on the capture stream grows that
+    stream's workspace, and workspaces of 20 more streams push it past the
+    LRU limit; then fresh allocations take whatever memory was freed and are
+    filled with a marker. Every replay still matches an eager call bit for
+    bit and leaves the marker tensors untouched: the reserved buffer was
+    neither freed nor reused."""
+    monkeypatch.setenv("FD_SPLIT_BLOCKS", "2")  # rows always split: the workspace is used
+    w = cases.Workload("graph", 12, 32, 8, 128, 16, torch.bfloat16, 64, 700, None, 19)
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    kc, vc, _kv = cases.kv_pool(w, pool, "vllm", gpu)
+    q = cases.queries(w, gpu)
+    bt_d, lens_d = bt.to(gpu), lens.to(gpu)
+    out = torch.empty(w.n, w.H, w.D, dtype=torch.float32, device=gpu)
+    lse = torch.empty(w.H, w.n, dtype=torch.float32, device=gpu)
+
+    def step():
+        ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, out=out, lse=lse)
+
+    ws = ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, bt.shape[1])
+    assert ws > 0
+    step()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=gpu)
+    reserved = ops.reserve_workspace(side, ws)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        step()
+    # growth: a call with 4x the rows on the capture stream needs a larger workspace
+    big_n = 4 * w.n
+    big_q = cases.queries(cases.Workload("graph", big_n, 32, 8, 128, 16, torch.bfloat16, 64,
+                                         700, None, 19), gpu)
+    big_bt = bt_d.repeat(4, 1)
+    big_lens = lens_d.repeat(4)
+    assert ops.workspace_bytes(big_n, w.H, w.KVH, w.D, w.BS, bt.shape[1]) > reserved.numel()
+    with torch.cuda.stream(side):
+        ops.paged_decode(big_q, kc, vc, big_bt, big_lens, w.scale)
+    side.synchronize()
+    key = (gpu.index or 0, side.cuda_stream)
+    assert ops.WORKSPACE._bufs[key].data_ptr() != reserved.data_ptr()  # it grew
+    # eviction pressure: more streams than the workspace keeps
+    streams = [torch.cuda.Stream(device=gpu) for _ in range(ops.WORKSPACE.max_streams + 4)]
+    for s in streams:
+        ops.WORKSPACE.get(gpu, reserved.numel(), stream=s.cuda_stream)
+    assert key in ops.WORKSPACE._bufs  # a reserved stream is never evicted
+    ptr = reserved.data_ptr()
+    del reserved
+    torch.cuda.synchronize()
+    # fresh allocations of the reserved buffer's size on its stream would reuse
+    # it if it had been freed (the caching allocator keeps freed blocks per stream)
+    with torch.cuda.stream(side):
+        markers = [torch.full((ws,), 77, dtype=torch.uint8, device=gpu) for _ in range(8)]
+    side.synchronize()
+    assert all(m.data_ptr() != ptr for m in markers)
+    gen = torch.Generator(device=gpu).manual_seed(9)
+    for r in range(3):
+        q.copy_(torch.randn(q.shape, generator=gen, device=gpu).to(q.dtype))
+        g.replay()
+        torch.cuda.synchronize()
+        got = (out.clone(), lse.clone())
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], out) and torch.equal(got[1], lse), f"replay {r}"
+        assert all(bool((m == 77).all()) for m in markers), f"replay {r} wrote into freed memory"
+    del g
+    ops.release_workspace(side)
+    for s in streams:
+        ops.WORKSPACE.release(gpu, s.cuda_stream)

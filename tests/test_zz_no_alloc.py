@@ -123,3 +123,42 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(gpu):
     assert "scratch" in str(e.value)
     torch.cuda.synchronize()
     assert torch.all(out == 7.0) and torch.all(lse == 7.0)
+
+
+@pytest.mark.parametrize("H,KVH,dtype", [(32, 8, torch.bfloat16), (32, 32, torch.float16)])
+def test_noalloc_in_a_graph_matches_eager(gpu, H, KVH, dtype):
+    """The entry point's use case: code under HIP graph capture. One eager
+    call first (the device's scratch address and launch settings are looked
+    up then), then the same call captured in a torch.cuda.CUDAGraph on a side
+    stream, for a shape whose rows split (the scratch holds split partials).
+    Each replay, with new queries and eager GPU work in between, is
+    bit-identical to an eager call on the same inputs."""
+    D = 128
+    n = 3
+    scale = 1.0 / math.sqrt(D)
+    q, kc, vc, bt, lens = _case(n, H, KVH, D, dtype, 5000, 8000, 21, gpu)
+    need = _workspace_bytes(n, H, KVH, D, 16, bt.shape[1])
+    assert 0 < need <= _lib.NOALLOC_SCRATCH_BYTES, need
+    qd, kd, vd = q.to(gpu), kc.to(gpu), vc.to(gpu)
+    btd, ld = bt.to(gpu), lens.to(gpu)
+    out = torch.empty((n, H, D), device=gpu)
+    lse = torch.empty((H, n), device=gpu)
+    _call(True, qd, kd, vd, btd, ld, scale, out, lse)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream(device=gpu)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        _call(True, qd, kd, vd, btd, ld, scale, out, lse)
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(256, 256, device=gpu)
+    for r in range(3):
+        qd.copy_(torch.randn(qd.shape, generator=gen, device=gpu).to(dtype))
+        g.replay()
+        torch.cuda.synchronize()
+        got = (out.clone(), lse.clone())
+        x = torch.tanh(x @ x) * 0.5  # eager work between the replay and the check
+        _call(True, qd, kd, vd, btd, ld, scale, out, lse)
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], out) and torch.equal(got[1], lse), f"replay {r}"
+    assert torch.isfinite(x).all()
+    del g

@@ -5,6 +5,8 @@
 // (the contract of fastdecode/csrc/cpu_attn.cpp:433-477 and :495-510, where
 // TORCH_CHECK raises before the kernel runs).
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -57,6 +59,14 @@ bool in_host_memory(const void* p) {
   cache[next] = {p, host};
   next = (next + 1) % kEntries;
   return host;
+}
+
+// Blocks made by fd_host_alloc and the device that was current then: the
+// device whose queued work fd_host_free waits for.
+std::mutex g_host_mu;
+std::unordered_map<void*, int>& host_blocks() {
+  static auto* m = new std::unordered_map<void*, int>();  // outlives static destructors
+  return *m;
 }
 
 // Mean fill of the table by the rows, from the caller's token total: the
@@ -435,37 +445,49 @@ int fd_host_alloc(size_t bytes, void** host_ptr) {
   if (host_ptr == nullptr) return set_error(FD_ERR_INVALID, "host_alloc: host_ptr is NULL");
   *host_ptr = nullptr;
   if (bytes == 0) bytes = 16;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_error(e, "host_alloc: hipGetDevice");
   unsigned flags = hipHostMallocMapped | hipHostMallocPortable;
   const char* nc = getenv("FD_HOST_NONCOHERENT");
   if (nc != nullptr && nc[0] == '1') flags |= hipHostMallocNonCoherent;
-  const hipError_t e = hipHostMalloc(host_ptr, bytes, flags);
+  e = hipHostMalloc(host_ptr, bytes, flags);
   if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
+  std::lock_guard<std::mutex> lock(g_host_mu);
+  host_blocks()[*host_ptr] = dev;
   return FD_OK;
 }
 
 int fd_host_free(void* host_ptr) {
   if (host_ptr == nullptr) return FD_OK;
-  // Kernels still enqueued on any device may read or write the block over
-  // the link: let them finish first (freeing is rare: a tier's teardown).
-  // If a wait fails (e.g. a stream capture is under way), the block is not
-  // freed: a leak, never a free under running kernels.
-  int count = 0, cur = 0;
-  hipError_t e = hipGetDeviceCount(&count);
-  if (e != hipSuccess) return hip_error(e, "host_free: hipGetDeviceCount");
-  e = hipGetDevice(&cur);
-  if (e != hipSuccess) return hip_error(e, "host_free: hipGetDevice");
-  for (int d = 0; d < count; ++d) {
-    e = hipSetDevice(d);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-      (void)hipSetDevice(cur);
-      return hip_error(e, "host_free: waiting for the device's work (block kept)");
-    }
+  int dev = 0;
+  {
+    std::lock_guard<std::mutex> lock(g_host_mu);
+    const auto it = host_blocks().find(host_ptr);
+    if (it == host_blocks().end())
+      return set_error(FD_ERR_INVALID, "host_free: %p was not allocated by fd_host_alloc",
+                       host_ptr);
+    dev = it->second;
   }
-  e = hipSetDevice(cur);
-  if (e != hipSuccess) return hip_error(e, "host_free: hipSetDevice");
+  // Kernels still enqueued on the tier's device may read or write the block
+  // over the link: let them finish first (freeing is rare: a tier's
+  // teardown). Only that device is waited for: a process that also reaches
+  // the block from other devices synchronises them itself. If the wait fails
+  // (e.g. a stream capture is under way), the block is not freed: a leak,
+  // never a free under running kernels.
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_error(e, "host_free: hipGetDevice");
+  e = dev == cur ? hipSuccess : hipSetDevice(dev);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  const hipError_t back = dev == cur ? hipSuccess : hipSetDevice(cur);
+  if (e != hipSuccess) return hip_error(e, "host_free: waiting for the device's work (block kept)");
+  if (back != hipSuccess) return hip_error(back, "host_free: hipSetDevice (block kept)");
   e = hipHostFree(host_ptr);
-  return e == hipSuccess ? FD_OK : hip_error(e, "hipHostFree");
+  if (e != hipSuccess) return hip_error(e, "hipHostFree");
+  std::lock_guard<std::mutex> lock(g_host_mu);
+  host_blocks().erase(host_ptr);
+  return FD_OK;
 }
 
 int fd_host_device_pointer(void* host_ptr, void** device_ptr) {

@@ -76,45 +76,79 @@ class _Workspace:
     allocator reuses a replaced one only after that stream's earlier work.
     At most `max_streams` buffers are kept; the least recently used one is
     dropped beyond that (its memory returns to its stream's pool, which only
-    that stream's later allocations reuse)."""
+    that stream's later allocations reuse).
+
+    A stream's buffer can be pinned (reserve_workspace, for HIP graph
+    capture): a captured graph keeps the raw address of the buffer its
+    launches were given, so a pinned stream's buffers are never dropped,
+    neither by the eviction above nor when growth replaces one, until the
+    reservation is released (release_workspace)."""
 
     def __init__(self, max_streams: int = 16) -> None:
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        # pinned (device, stream) -> every buffer the stream has held since
+        self._pinned: dict[tuple[int, int], list[torch.Tensor]] = {}
         self._lock = threading.Lock()
         self.max_streams = max_streams
 
-    def get(self, device: torch.device, nbytes: int, stream: int | None = None
-            ) -> torch.Tensor | None:
+    @staticmethod
+    def _key(device: torch.device, stream: int | None) -> tuple[int, int]:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return idx, _current_stream(idx) if stream is None else int(stream)
+
+    def get(self, device: torch.device, nbytes: int, stream: int | None = None,
+            pin: bool = False) -> torch.Tensor | None:
         """The workspace of `stream` (a raw handle; default: the current
         stream on `device`, the one the caller's launch goes on), at least
-        nbytes long."""
-        if nbytes == 0:
+        nbytes long. pin: keep this stream's buffers alive (see above)."""
+        if nbytes == 0 and not pin:
             return None
-        idx = device.index if device.index is not None else torch.cuda.current_device()
-        key = (idx, _current_stream(idx) if stream is None else int(stream))
+        key = self._key(device, stream)
         with self._lock:
             buf = self._bufs.pop(key, None)  # re-inserted below: most recent last
             if buf is None or buf.numel() < nbytes:
-                cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
-                buf = torch.empty(cap, dtype=torch.uint8, device=torch.device("cuda", idx))
+                cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0), 16)
+                buf = torch.empty(cap, dtype=torch.uint8, device=torch.device("cuda", key[0]))
+                if key in self._pinned:
+                    self._pinned[key].append(buf)
+            if pin and key not in self._pinned:
+                self._pinned[key] = [buf]
             self._bufs[key] = buf
             while len(self._bufs) > self.max_streams:
-                del self._bufs[next(iter(self._bufs))]
+                victim = next((k for k in self._bufs if k not in self._pinned), None)
+                if victim is None:
+                    break
+                del self._bufs[victim]
             return buf
+
+    def release(self, device: torch.device, stream: int) -> None:
+        """Ends a pin: the stream's replaced buffers go, its current one stays
+        (and may be evicted again)."""
+        with self._lock:
+            self._pinned.pop(self._key(device, stream), None)
 
 
 WORKSPACE = _Workspace()
 
 
-def reserve_workspace(stream: torch.cuda.Stream, nbytes: int) -> None:
+def reserve_workspace(stream: torch.cuda.Stream, nbytes: int) -> torch.Tensor:
     """Allocates the split workspace of `stream` now, at least nbytes long
-    (workspace_bytes of the largest shape to come). For HIP graph capture:
-    torch.cuda.graph captures on its own stream, so a workspace reserved for
-    that stream before capture keeps the captured launches from allocating
-    (otherwise the first captured launch of a shape that splits rows
-    allocates it from the graph's memory pool)."""
+    (workspace_bytes of the largest shape to come), and pins it. For HIP
+    graph capture: torch.cuda.graph captures on its own stream, so a
+    workspace reserved for that stream before capture keeps the captured
+    launches from allocating (otherwise the first captured launch of a shape
+    that splits rows allocates it from the graph's memory pool). The graph
+    keeps the buffer's raw address, so while the reservation holds, the
+    buffer is neither evicted nor freed when a later, larger call on the
+    same stream grows the workspace. Returns the buffer; call
+    release_workspace(stream) once every graph captured with it is gone."""
     with torch.cuda.stream(stream):
-        WORKSPACE.get(stream.device, nbytes)
+        return WORKSPACE.get(stream.device, nbytes, pin=True)
+
+
+def release_workspace(stream: torch.cuda.Stream) -> None:
+    """Ends reserve_workspace's pin on `stream`'s workspace."""
+    WORKSPACE.release(stream.device, stream.cuda_stream)
 
 
 _WS_SIZES: dict = {}
@@ -143,9 +177,13 @@ def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtyp
 
 
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
-    """Workspace a decode call of this shape needs (remembered per shape and
-    task-size override, which the library reads from FD_SPLIT_BLOCKS)."""
-    key = (n, H, KVH, D, BS, width, os.environ.get("FD_SPLIT_BLOCKS"))
+    """Workspace a decode call of this shape needs on the current device
+    (remembered per shape, device and the planner overrides it depends on:
+    FD_SPLIT_BLOCKS, and FD_DECODE_KERNEL, which can allow more splits; the
+    device's CU count sets the split bounds)."""
+    dev = torch.cuda.current_device() if torch.cuda.is_available() else -1
+    key = (n, H, KVH, D, BS, width, os.environ.get("FD_SPLIT_BLOCKS"),
+           os.environ.get("FD_DECODE_KERNEL"), dev)
     size = _WS_SIZES.get(key)
     if size is None:
         c = ctypes.c_size_t()
