@@ -15,6 +15,7 @@ count.
 
 from __future__ import annotations
 
+import ctypes
 import math
 
 import pytest
@@ -231,3 +232,29 @@ def test_host_decode_in_a_forked_child():
             proc.kill()
     assert proc.exitcode == 0
     assert torch.equal(child[0], parent[0]) and torch.equal(child[1], parent[1])
+
+
+def test_host_stream_read_checksum_and_arguments():
+    """fd_host_stream_read (the host-DRAM read-rate probe): the checksum is the
+    XOR of the buffer's 64-bit words, whatever the thread count and whether
+    the size is a whole number of its 1 MiB chunks; bad sizes, unaligned
+    sources and too many threads are argument errors."""
+    import numpy as np
+
+    from vllm_fastdecoder_amd import _lib, ops
+
+    g = torch.Generator().manual_seed(3)
+    for nbytes in (64, 4096, (3 << 20) + 192):
+        words = torch.randint(-(2 ** 62), 2 ** 62, (nbytes // 8,), generator=g, dtype=torch.int64)
+        want = int(np.bitwise_xor.reduce(words.numpy().view(np.uint64)))
+        for threads in (1, 3, 0):
+            assert ops.host_stream_read(words, threads) == want
+    lib = _lib.load_lib()
+    buf = torch.zeros(1024, dtype=torch.int64)
+    out = ctypes.c_uint64(7)
+    assert lib.fd_host_stream_read(buf.data_ptr(), 100, 1, ctypes.byref(out)) == _lib.FD_ERR_INVALID
+    assert lib.fd_host_stream_read(buf.data_ptr() + 8, 64, 1, ctypes.byref(out)) == \
+        _lib.FD_ERR_INVALID
+    assert lib.fd_host_stream_read(buf.data_ptr(), 64, 1 << 20, ctypes.byref(out)) == \
+        _lib.FD_ERR_INVALID
+    assert lib.fd_host_stream_read(None, 0, 1, ctypes.byref(out)) == _lib.FD_OK and out.value == 0

@@ -198,6 +198,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "fd_host_decode_threads": (c_int, []),
     "fd_host_decode_isa": (c_int, []),
+    "fd_host_stream_read": (c_int, [c_void_p, c_size_t, c_int32, POINTER(ctypes.c_uint64)]),
     "fd_host_set_threads": (c_int, [c_int32]),
     "fd_share_host_blocks": (
         c_int,

@@ -534,6 +534,46 @@ extern "C" int fd_host_store_kv(const void* k, int64_t k_stride_tok, int64_t k_s
 
 extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 
+// Plain multi-threaded read of a host buffer on the pool that runs the
+// host-core kernel: 1 MiB chunks handed out from an atomic counter, each
+// read as 64-bit words into eight independent XOR chains (no other work per
+// byte), so the rate is the cores' DRAM read rate for a streamed buffer. The
+// XOR of all words comes back as a checksum (order independent).
+extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_threads,
+                                   uint64_t* checksum) {
+  if (bytes % 64 != 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
+    return set_error(FD_ERR_INVALID, "fd_host_stream_read: bytes %% 64 != 0 or bad thread count");
+  if (bytes > 0 && (src == nullptr || reinterpret_cast<uintptr_t>(src) % 64 != 0))
+    return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL or unaligned (64 B) source");
+  if (checksum == nullptr) return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL checksum");
+  *checksum = 0;
+  if (bytes == 0) return FD_OK;
+  constexpr size_t kChunk = 1 << 20;
+  const int64_t chunks = (int64_t)((bytes + kChunk - 1) / kChunk);
+  const int nt = (int)std::max<int64_t>(
+      1, std::min<int64_t>(num_threads > 0 ? num_threads : default_threads(), chunks));
+  std::atomic<int64_t> next{0};
+  std::atomic<uint64_t> total{0};
+  const uint64_t* words = static_cast<const uint64_t*>(src);
+  PoolState& ps = pool_state();
+  std::lock_guard<std::mutex> call(ps.call_mu);
+  ps.pool.run(nt, [&](int) {
+    uint64_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (;;) {
+      const int64_t c = next.fetch_add(1, std::memory_order_relaxed);
+      if (c >= chunks) break;
+      const size_t lo = (size_t)c * kChunk / 8;
+      const size_t hi = std::min(bytes, (size_t)(c + 1) * kChunk) / 8;
+      for (size_t w = lo; w < hi; w += 8)
+        for (int j = 0; j < 8; ++j) x[j] ^= words[w + j];
+    }
+    total.fetch_xor(x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7],
+                    std::memory_order_relaxed);
+  });
+  *checksum = total.load(std::memory_order_relaxed);
+  return FD_OK;
+}
+
 extern "C" int fd_host_decode_partial(
     const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
     const void* v_cache, int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,

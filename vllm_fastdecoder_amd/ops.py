@@ -979,7 +979,25 @@ def store_kv(k, v, slots, k_cache, v_cache) -> None:
 
 
 def stream_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
-    """Byte copy with the attention kernels' 16-byte loads (measurement aid)."""
+    """Byte copy on the GPU with the attention kernels' 16-byte loads
+    (measurement aid). Either side may be pinned host memory (read or written
+    over the link); the copy runs on the current stream of the GPU side."""
     nbytes = src.numel() * src.element_size()
     _require(dst.numel() * dst.element_size() >= nbytes, "dst too small")
-    _lib.check(_lib.load_lib().fd_stream_copy(dst.data_ptr(), src.data_ptr(), nbytes, _stream_for(src)))
+    gpu_side = dst if dst.is_cuda else src
+    _require(gpu_side.is_cuda or torch.cuda.is_available(), "stream_copy needs a GPU")
+    stream = _stream_for(gpu_side) if gpu_side.is_cuda else \
+        torch.cuda.current_stream().cuda_stream
+    _lib.check(_lib.load_lib().fd_stream_copy(device_ptr(dst), device_ptr(src), nbytes, stream))
+
+
+def host_stream_read(t: torch.Tensor, num_threads: int = 0) -> int:
+    """Reads every byte of the contiguous host tensor t (64-byte aligned, a
+    multiple of 64 bytes long) on the host cores (fd_host_stream_read) and
+    returns the XOR of its 64-bit words: the host cores' DRAM read rate, the
+    bound of the host-core leg of the split step (measurement aid)."""
+    _require(not t.is_cuda and t.is_contiguous(), "host_stream_read: contiguous host tensor")
+    out = ctypes.c_uint64()
+    _lib.check(_lib.load_lib().fd_host_stream_read(t.data_ptr(), t.numel() * t.element_size(),
+                                                   int(num_threads), ctypes.byref(out)))
+    return int(out.value)
