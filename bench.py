@@ -20,7 +20,13 @@ Printed (one JSON line):
                (scripts/probe_cpu_attn.py:63-68)
   split_run    the same batch with 60% of each row's blocks (its last ones)
                in pinned host memory read zero-copy over the link: HBM
-               partial + host partial + merge, with the link rate
+               partial + host partial + merge, with the link rate; the
+               fused and hybrid steps; the reference's own split step on
+               this box (cpu_attn.cpp over the host tier); and the split
+               step's roofline against the host tier's read rates measured
+               here (host cores, link, both at once)
+Each leg (small batch, Llama-3-8B) carries its own roofline and, like the
+headline, a cpu_baseline: the reference's cpu_attn.cpp on the leg's data.
 """
 
 from __future__ import annotations
@@ -269,6 +275,127 @@ def hybrid_profile(w, lens, bt, q, frac, steps, warmup, stream):
             "host_cores_ms": round(cpu_ms, 3), "host_cores": threads_used()}
 
 
+def host_tier_peaks(hk, hv, dev, threads, reps=5):
+    """The read rates that bound the split step's host tier, on this box:
+    the host cores streaming the pinned tier from DRAM (fd_host_stream_read
+    over K and V, on the threads the host-core kernel uses), the GPU reading
+    it over the link (fd_stream_copy from pinned memory into HBM), and both
+    at once (the cores re-reading K in 128 MiB pieces while the GPU copies V
+    four times; each side's bytes over its own time)."""
+    import torch
+
+    from vllm_fastdecoder_amd import ops
+
+    k8 = hk.view(-1).view(torch.uint8)
+    v8 = hv.view(-1).view(torch.uint8)
+    kb, vb = k8.numel(), v8.numel()
+    ops.host_stream_read(k8, threads)
+    cores = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        ops.host_stream_read(k8, threads)
+        ops.host_stream_read(v8, threads)
+        cores.append(time.perf_counter() - t0)
+    cores.sort()
+    t_cores = cores[len(cores) // 2]
+    dst = torch.empty(vb, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    t_link = time_gpu(lambda: ops.stream_copy(dst, v8), reps, 1, stream)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(4):
+        ops.stream_copy(dst, v8)
+    end.record(stream)
+    piece = min(kb, 128 << 20) // 64 * 64
+    cpu_bytes, off = 0, 0
+    t0 = time.perf_counter()
+    while not end.query():
+        if off + piece > kb:
+            off = 0
+        ops.host_stream_read(k8[off: off + piece], threads)
+        off += piece
+        cpu_bytes += piece
+    t_cpu = time.perf_counter() - t0
+    end.synchronize()
+    t_gpu = start.elapsed_time(end) / 1e3
+    del dst
+    cores_gbps = (kb + vb) / t_cores / 1e9
+    link_gbps = vb / (t_link / 1e3) / 1e9
+    conc_cores = cpu_bytes / t_cpu / 1e9 if t_cpu > 0 else 0.0
+    conc_link = 4 * vb / t_gpu / 1e9
+    return {
+        "host_dram_read_GBps": round(cores_gbps, 1),
+        "link_read_GBps": round(link_gbps, 2),
+        "concurrent_GBps": round(conc_cores + conc_link, 1),
+        "concurrent_cores_GBps": round(conc_cores, 1),
+        "concurrent_link_GBps": round(conc_link, 2),
+        "threads": threads,
+    }
+
+
+def cpu_baseline_split_step(w, q, kc_g, vc_g, bt_g_d, len_g_d, ord_g, hk, hv, bt_c, len_c,
+                            threads, steps=10):
+    """The reference's own split step, timed on this box
+    (fastdecode/backend.py:287-356): the query copied to pinned staging
+    without blocking, the GPU-tier partial launched (this library's kernel:
+    the reference's FlashAttention call is CUDA-only), then, once the copy has
+    landed, cpu_attn.cpp's decode_attn (built from its source) over the host
+    tier on the host cores, the host partial copied back and merged on the
+    GPU. The GPU partial overlaps the host-core work, as in the reference.
+    Returns (step ms, host-core call ms, kind)."""
+    import torch
+
+    import oracle
+    from vllm_fastdecoder_amd import ops
+
+    dev = q.device
+    ext = oracle.ref_ext()
+    kind = "reference" if ext is not None else "port"
+    if ext is not None:
+        ext.set_num_threads(threads)
+    hq = torch.empty(q.shape, dtype=q.dtype).pin_memory()
+    out_dt = q.dtype if ext is not None else torch.float32
+    ho = torch.empty(w.n, w.H, w.D, dtype=out_dt).pin_memory()
+    hl = torch.empty(w.H, w.n, dtype=torch.float32).pin_memory()
+    o_g = torch.empty(w.n, w.H, w.D, dtype=q.dtype, device=dev)
+    l_g = torch.empty(w.H, w.n, dtype=torch.float32, device=dev)
+    o_c = torch.empty(w.n, w.H, w.D, dtype=out_dt, device=dev)
+    l_c = torch.empty_like(l_g)
+    merged = torch.empty_like(o_g)
+    cpu_s = []
+
+    def step():
+        hq.copy_(q, non_blocking=True)
+        staged = torch.cuda.Event()
+        staged.record()
+        ops.paged_decode(q, kc_g, vc_g, bt_g_d, len_g_d, w.scale, out=o_g, lse=l_g,
+                         row_order=ord_g)
+        staged.synchronize()
+        t0 = time.perf_counter()
+        if ext is not None:
+            ext.decode_attn(hq, hk, hv, bt_c, len_c, w.scale, ho, hl)
+        else:
+            oracle.decode_attn_cpu_f32(hq, hk, hv, bt_c, len_c, w.scale, ho, hl, threads=threads)
+        cpu_s.append(time.perf_counter() - t0)
+        o_c.copy_(ho, non_blocking=True)
+        l_c.copy_(hl, non_blocking=True)
+        ops.merge_attn_states(merged, o_g, l_g, o_c, l_c)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    cpu_s.clear()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t_step = (time.perf_counter() - t0) / steps
+    cpu_s.sort()
+    return t_step * 1e3, cpu_s[len(cpu_s) // 2] * 1e3, kind
+
+
 def split_run(w, lens, bt, q, steps, warmup, stream):
     """The split-run layout (split_tiers): HBM partial + host partial
     (zero-copy) + LSE merge, the same step as one fused launch
@@ -364,6 +491,11 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     planner = time_planners(w, bt_g, len_g, bt_c, len_c, G, C, dev)
     b_hbm, kv_hbm = algorithmic_bytes(len_g, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
     b_host, kv_host = algorithmic_bytes(len_c, w.n, w.H, w.KVH, w.D, w.BS, 2, 2)
+    threads = threads_used()
+    peaks = host_tier_peaks(hk, hv, dev, threads)
+    ref_ms, ref_cpu_ms, ref_kind = cpu_baseline_split_step(w, q, kc_g, vc_g, bt_g_d, len_g_d,
+                                                           ord_g, hk, hv, bt_c, len_c, threads)
+    host_gbps = kv_host / (t_auto / 1e3) / 1e9
     del kv, hk, hv, q_host
     return {
         "host_fraction_blocks": 0.6,
@@ -387,6 +519,34 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "hybrid_auto_cpu_fraction": [round(min(auto_fracs), 3), round(max(auto_fracs), 3)],
         "hybrid_auto_tokens_per_s": round(w.n / (t_auto / 1e3 * LAYERS), 1),
         "hybrid_auto_GBps": round((kv_hbm + kv_host) / (t_auto / 1e3) / 1e9, 1),
+        "host_tier_bytes": kv_host,
+        "roofline": {
+            "bound": "host DRAM (host cores and the link reading the pinned tier, measured "
+                     "together on this box)",
+            "achieved": round(host_gbps, 1),
+            "peak": peaks["concurrent_GBps"],
+            "unit": "GB/s",
+            "frac": round(host_gbps / peaks["concurrent_GBps"], 4),
+            "frac_of_host_dram": round(host_gbps / peaks["host_dram_read_GBps"], 4),
+            "kernel_ms": round(t_auto, 4),
+            "note": "achieved = host-tier K+V bytes / hybrid step (share balanced online); "
+                    "the HBM tier is read at the same time",
+            **peaks,
+        },
+        "reference_step_ms": round(ref_ms, 3),
+        "reference_step": {
+            "ms": round(ref_ms, 3),
+            "tokens_per_s": round(w.n / (ref_ms / 1e3 * LAYERS), 1),
+            "host_share_ms": round(ref_cpu_ms, 3),
+            "host_share_GBps": round(kv_host / (ref_cpu_ms / 1e3) / 1e9, 2),
+            "cores": threads,
+            "kind": ref_kind,
+            "note": ("fastdecode/backend.py:287-356 on this box: q to pinned staging, GPU-tier "
+                     "partial (this library's kernel in place of the CUDA-only FlashAttention), "
+                     "cpu_attn.cpp decode_attn over the host tier on the host cores, (out, lse) "
+                     "back, merge on the GPU; the hybrid step is "
+                     f"{ref_ms / t_auto:.2f}x faster"),
+        },
         "planner": planner,
         "note": ("host tier read zero-copy from hipHostMalloc memory; PCIe-inclusive, not "
                  "`value`; host_cores = fd_host_decode_partial over the whole host tier; "
@@ -634,6 +794,15 @@ def main() -> int:
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, lens, bt, pool, q.cpu(), args.cpu_iters)
+        # the same protocol on each leg's workload (its own seeded inputs)
+        for key, name in (("small_batch_leg", "correctness"), ("llama3_8b_leg", "llama3_8b")):
+            if key in result:
+                lw = cases.WORKLOADS[name]
+                l_lens, l_bt, l_pool = cases.draw_lens_and_tables(lw)
+                result[key]["cpu_baseline"] = cpu_baseline(lw, l_lens, l_bt, l_pool,
+                                                           cases.queries(lw, "cpu"),
+                                                           args.cpu_iters)
+                torch.cuda.empty_cache()
     print(json.dumps(result), flush=True)
     return 0
 

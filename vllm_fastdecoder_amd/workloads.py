@@ -97,8 +97,11 @@ def split_tiers(w: Workload, lens: torch.Tensor, bt: torch.Tensor, dev):
     each row in pinned host memory [C, KVH, BS, D], the rest in the HBM
     tier's vLLM layout [G, BS, KVH, 2D], each tier's table compacted in
     sequence order (the planner's s_gpu_bt / s_cpu_bt) and its token counts
-    (HBM blocks are whole; the host tier holds the partial last block). Data
-    N(0,1), seeded. bt only gives the table width."""
+    (HBM blocks are whole; the host tier holds the partial last block). A
+    row's blocks in each tier are scattered: consecutive runs of a seeded
+    random permutation of that tier's ids, as the all-HBM run draws them and
+    as an allocator that reuses freed blocks hands them out. Data N(0,1),
+    seeded. bt only gives the table width."""
     from vllm_fastdecoder_amd.pinned import pinned_empty
 
     nb = (lens + w.BS - 1) // w.BS
@@ -111,11 +114,14 @@ def split_tiers(w: Workload, lens: torch.Tensor, bt: torch.Tensor, dev):
     len_c = (lens - len_g).to(torch.int32)
     G = int(n_hbm.sum())
     C = int(n_host.sum())
+    g = torch.Generator().manual_seed(7000 + w.seed)
+    perm_g = torch.randperm(max(G, 1), generator=g).to(torch.int32)
+    perm_c = torch.randperm(max(C, 1), generator=g).to(torch.int32)
     pg = pc = 0
     for i in range(w.n):
         a, b = int(n_hbm[i]), int(n_host[i])
-        bt_g[i, :a] = torch.arange(pg, pg + a, dtype=torch.int32)
-        bt_c[i, :b] = torch.arange(pc, pc + b, dtype=torch.int32)
+        bt_g[i, :a] = perm_g[pg : pg + a]
+        bt_c[i, :b] = perm_c[pc : pc + b]
         pg += a
         pc += b
     kc_g, vc_g, kv = kv_pool(w, max(G, 1), "vllm", dev)
