@@ -4,6 +4,8 @@ it, is checked by tests/test_gpu_decode_mm.py)."""
 
 from __future__ import annotations
 
+import math
+
 import pytest
 import torch
 
@@ -245,3 +247,77 @@ def test_d64_rows_split_only_when_the_total_shows_them_full(gpu):
         mixed = ops.decode_plan_info(n, 14, 2, 64, 16, 256, torch.bfloat16,
                                      total_tokens=int(0.85 * full))
         assert mixed == base, (n, mixed, base)
+
+
+@pytest.mark.gpu
+def test_every_window_boundary_from_both_sides(gpu):
+    """Each window of the planner's cut table (decode_partial.hip, "row
+    cuts") just inside and just outside each of its bounds, on a 256-block
+    table (4096 tokens): rows per CU 1.0 / 1.3 (quarter rows at D = 128 and
+    64), 2.0 / 2.6 (half rows), 1.5 (slot fill); mean fill 0.8 (half rows on
+    one side, slot fill on the other) and 0.95 (D = 64). Inside a quarter
+    window tasks are 64 blocks (4 per row), inside a half window 128 (2 per
+    row); outside, the model's whole rows (or, at D = 64, the plan without a
+    total)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    W = 256
+
+    def plan(n, H, KVH, D, fill=None, below=False):
+        total = None
+        if fill is not None:
+            cap = n * W * 16
+            total = math.floor(fill * cap) - 1 if below else math.ceil(fill * cap)
+        return ops.decode_plan_info(n, H, KVH, D, 16, W, torch.bfloat16, total_tokens=total)
+
+    def cut(p):
+        return (p["split_blocks"], p["max_splits"])
+
+    def rows_n(kvh, lo10, hi10):
+        """Sequence counts just outside and just inside each side of the
+        window lo10 / 10 < rows per CU <= hi10 / 10 (rows = n * kvh)."""
+        ns = [n for n in range(1, 4 * cus) if n * kvh * 10 > lo10 * cus and
+              n * kvh * 10 <= hi10 * cus]
+        first, last = ns[0], ns[-1]
+        return first - 1, first, last, last + 1
+
+    # quarter rows at D = 128 (8 query heads on 1 kv head: the matrix-core kernel), any fill
+    out_lo, in_lo, in_hi, out_hi = rows_n(1, 10, 13)
+    for n in (in_lo, in_hi):
+        assert cut(plan(n, 8, 1, 128)) == (64, 4), n
+    for n in (out_lo, out_hi):
+        assert cut(plan(n, 8, 1, 128)) == (256, 1), n
+    # ... and on the VALU kernel (MHA, 32 kv heads)
+    out_lo, in_lo, in_hi, out_hi = rows_n(32, 10, 13)
+    assert cut(plan(in_lo, 32, 32, 128)) == (64, 4) and cut(plan(in_hi, 32, 32, 128)) == (64, 4)
+    assert plan(out_hi, 32, 32, 128)["split_blocks"] != 64
+    # quarter rows at D = 64 (14 query heads on 2 kv heads): fill 0.95 or more
+    out_lo, in_lo, in_hi, out_hi = rows_n(2, 10, 13)
+    for n in (in_lo, in_hi):
+        assert cut(plan(n, 14, 2, 64, 0.95)) == (64, 4), n
+        assert plan(n, 14, 2, 64, 0.95, below=True) == plan(n, 14, 2, 64), n
+    for n in (out_lo, out_hi):
+        assert plan(n, 14, 2, 64, 1.0) == plan(n, 14, 2, 64), n
+    # half rows at D = 128: fill 0.8 or more
+    out_lo, in_lo, in_hi, out_hi = rows_n(1, 20, 26)
+    for n in (in_lo, in_hi):
+        assert cut(plan(n, 8, 1, 128, 0.8)) == (128, 2), n
+        assert cut(plan(n, 8, 1, 128, 0.8, below=True)) == (256, 1), n
+    for n in (out_lo, out_hi):
+        assert cut(plan(n, 8, 1, 128, 1.0)) == (256, 1), n
+    # half rows at D = 64: fill 0.95 or more
+    out_lo, in_lo, in_hi, out_hi = rows_n(2, 20, 26)
+    for n in (in_lo, in_hi):
+        assert cut(plan(n, 14, 2, 64, 0.95)) == (128, 2), n
+        assert plan(n, 14, 2, 64, 0.95, below=True) == plan(n, 14, 2, 64), n
+    for n in (out_lo, out_hi):
+        assert plan(n, 14, 2, 64, 1.0) == plan(n, 14, 2, 64), n
+    # slot fill: fill below 0.8, at most 1.5 rows per CU, on the matrix-core kernel
+    _, _, in_hi, out_hi = rows_n(1, 0, 15)
+    base = plan(in_hi, 8, 1, 128)
+    assert plan(in_hi, 8, 1, 128, 0.6)["max_splits"] > 1
+    assert plan(in_hi, 8, 1, 128, 0.8, below=True)["max_splits"] > 1
+    assert plan(in_hi, 8, 1, 128, 0.8) == base
+    assert plan(out_hi, 8, 1, 128, 0.6) == plan(out_hi, 8, 1, 128)
+    half_cu = cus // 2
+    assert plan(half_cu, 8, 1, 128, 0.8, below=True)["max_splits"] > 1
+    assert plan(half_cu, 8, 1, 128, 0.8) == plan(half_cu, 8, 1, 128)

@@ -298,6 +298,71 @@ int tiled_wgs_per_cu(const SplitPlan& sp, int32_t kv_dtype, int32_t D) {
   return dispatch_tiled(tp, 0, q, kv_dtype, D, false, nullptr) == hipSuccess ? wgs : 0;
 }
 
+// ---------------------------------------------------------------- row cuts
+// The windows in which the plan departs from the launch-time model below
+// (model_split_blocks: whole rows unless few long rows need splitting), all
+// in this block. A "row" is a (sequence, kv head, head-group pass) of the
+// launch; rows per CU = rows / the device's CUs; fill = the rows' mean
+// length over the table width, from the caller's token total (0: unknown).
+// Row windows are open below and closed above (lo < rows per CU <= hi),
+// fill windows closed below. tests/test_plan_info.py pins both sides of
+// every boundary.
+//
+//   plan          kernel            D      rows per CU   fill          tasks
+//   slot fill     mm, 16 heads      any    (0, 1.5]      (0, 0.8)      3 WGs/CU, 65-130 % filled, <= 8 per row
+//   quarter rows  VALU or mm        128    (1.0, 1.3]    any           4 per row of the table, 3 WGs/CU
+//   quarter rows  VALU or mm        64     (1.0, 1.3]    [0.95, 1]     4 per row, 3 WGs/CU
+//   half rows     VALU or mm        128    (2.0, 2.6]    [0.8, 1]      2 per row, 3 WGs/CU
+//   half rows     VALU or mm        64     (2.0, 2.6]    [0.95, 1]     2 per row, 3 WGs/CU
+//   wave blocks   VALU              128    tasks <= CUs  any           a task's waves work by row length
+//
+// Why each window (measured on MI355X, bf16 unless stated, HIP graph replay,
+// the same call with and without the plan):
+//   * slot fill: the matrix-core kernel's per-block chain (scores MFMAs, the
+//     cross-row max, the LDS round trip of V, the P.V MFMAs) makes one
+//     workgroup a slow stream, so uneven rows leave the CUs holding the
+//     longest ones working long after the rest; three workgroups per CU,
+//     each with a share, end together. 8 / 1 heads, batch 256, rows of
+//     U[1024, 4096]: 67.4 -> 61.7 us; +8 to +17 % over 17 shapes of rows of
+//     U[L/4, L] and U[L/16, L]. Equal rows lose under it (86.7 -> 101.2 us at
+//     4096 tokens: a second round of whole tasks), so it needs the total.
+//     Past 1.5 rows per CU mixed rows balance by themselves (-3 to -6 % split
+//     at two per CU); a cut into one task per row would drop the model's
+//     two-per-CU cap (-9 to -12 %), so a fill always splits.
+//   * quarter rows: with whole rows, the rows past one per CU land as second
+//     workgroups on CUs that already stream one, and those CUs take about
+//     twice as long. 8 / 1 heads at 272 rows of 4096 tokens 136.4 -> 104.2 us;
+//     MHA (VALU) at 288 rows 121.6 -> 100.2 us; the gain is gone by about 1.5
+//     rows per CU. At D = 64 quarters lost on near-full rows of mixed length
+//     (fill 0.8-0.9: up to -20 %) and gained 10-20 % on equal ones, hence the
+//     0.95 fill there.
+//   * half rows: the same effect past two rows per CU under the two-per-CU
+//     cap, for full rows only (8 / 1 heads, 528-640 rows of 4096 tokens:
+//     216.1 / 264.9 / 278.0 -> 196.3 / 205.8 / 210.1 us); rows of mixed length
+//     balance by themselves and lose 3-11 % split.
+//   * wave blocks: see plan_decode.
+constexpr int kFillPerCu = 3;            // workgroups per CU the cut plans run at
+constexpr int32_t kMinFillBlocks = 16;   // smallest task a cut makes (16-token tiles)
+constexpr int32_t kMaxFillSplits = 8;    // slot fill: at most this many tasks per row
+constexpr double kMaxFillRows = 0.8;     // slot fill: mean fill below this (rows uneven)
+constexpr int kMaxFillRowsPerCu10 = 15;  // slot fill: at most 1.5 rows per CU (in tenths)
+constexpr double kMinFillSlots = 0.65;   // slot fill: expected tasks as a share of the
+constexpr double kMaxFillSlots = 1.3;    // three-per-CU slots, at least / at most
+
+// The quarter- and half-row windows of the table above.
+struct RowCut {
+  int32_t head_size;  // the head size the window applies to
+  int lo10, hi10;     // lo10 / 10 < rows per CU <= hi10 / 10
+  double fill_lo;     // mean fill >= fill_lo (0: the total may be unknown)
+  int32_t parts;      // a row of the table's width is cut into this many tasks
+};
+constexpr RowCut kRowCuts[] = {
+    {128, 10, 13, 0.0, 4},
+    {64, 10, 13, 0.95, 4},
+    {128, 20, 26, 0.8, 2},
+    {64, 20, 26, 0.95, 2},
+};
+
 // Tasks a launch is expected to run with S tasks per full row when its rows
 // fill `fill` of the table width on average (a row of fill x has ceil(x S)
 // tasks; about fill * S + 1/2 per row).
@@ -305,35 +370,18 @@ double expected_tasks(int32_t n, int32_t kv_tasks, int64_t S, double fill) {
   return (double)n * kv_tasks * (S <= 1 ? 1.0 : std::min((double)S, fill * S + 0.5));
 }
 
-constexpr int kFillPerCu = 3;          // workgroups per CU the slot fill runs at
-constexpr int32_t kMinFillBlocks = 16;  // smallest task the slot fill makes (blocks)
-constexpr int32_t kMaxFillSplits = 8;  // nor splits a row into more tasks than this
-constexpr double kMaxFillRows = 0.8;   // mean row fill below which rows count as uneven
-constexpr double kMinFillSlots = 0.65;  // expected tasks of a slot fill, as a share of the
-constexpr double kMaxFillSlots = 1.3;   // slots: at least / at most
-constexpr double kFullRowsD64 = 0.95;   // fill at which D = 64 rows count as full
+// Whether the slot fill's window holds: uneven rows (fill known and below
+// 0.8) on the one-column-group matrix-core kernel, at up to 1.5 rows per CU.
+bool slot_fill_window(const SplitPlan& sp, int64_t rows, int cus, double fill) {
+  return fill > 0.0 && fill < kMaxFillRows && sp.mm && sp.kernel_g == 16 && cus > 0 &&
+         rows * 10 <= (int64_t)kMaxFillRowsPerCu10 * cus;
+}
 
-// The slot fill of the matrix-core kernel with one 16-head column group, for
-// rows of uneven length (mean fill of the table width known from the caller
-// and below 0.8): blocks per task such that the expected tasks make 65-130 %
+// The slot fill: blocks per task such that the expected tasks make 65-130 %
 // of one round of three workgroups per CU and no row splits more than eight
 // ways, or 0 when no task size that splits rows does; the coarsest such size
 // wins. (Past one round the few extra tasks are short ones: at 1.05-1.27
-// rounds split tasks still beat the model's whole rows by 14-32 %, 8 / 1,
-// 12 / 2 and 28 / 4 heads, batch 68-320.) One workgroup of this kernel is a slow stream (its
-// per-block chain: scores MFMAs, the cross-row max, the LDS round trip of V,
-// the P.V MFMAs), so uneven rows leave the CUs holding the longest ones
-// working long after the rest; three per CU, each with a share of the work,
-// end together. Measured on MI355X (bf16, HIP graph replay, the same call
-// with and without the total): 8 query heads on 1 kv head, batch 256, rows
-// of U[1024, 4096] tokens 67.4 -> 61.7 us (64-block tasks, three per CU,
-// against whole rows under the two-per-CU cap), rows of U[256, 4096] 63.7 ->
-// 57.1 us; over 17 shapes of 8/1, 12/2, 28/4, 32/8, 64/8 at D = 128 and 14/2
-// at D = 64 the fill took +8 to +17 % where it applied, for rows of
-// U[L/4, L] and U[L/16, L], and left the others within 0.5 %. Rows of equal
-// length lose under it (86.7 -> 101.2 us at 4096 tokens: every row splits
-// into whole tasks and a second round returns); they keep the model's plan,
-// which is why the fill needs the caller's total.
+// rounds split tasks still beat the model's whole rows by 14-32 %.)
 int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots, double fill) {
   const int64_t W = wt > 0 ? wt : 1;
   for (int32_t sb = kMaxSplitBlocks; sb >= kMinFillBlocks; sb /= 2) {
@@ -341,50 +389,27 @@ int32_t fill_split_blocks(int32_t n, int32_t kv_tasks, int32_t wt, int64_t slots
     if (S > kMaxFillSplits) break;
     const double tasks = expected_tasks(n, kv_tasks, S, fill);
     if (tasks > kMaxFillSlots * (double)slots) break;  // finer sizes only add tasks
-    // a fill splits rows; whole rows stay with the model and its cap (rows of
-    // mixed length at 2-2.6 per CU: -9 to -12 % without the cap)
     if (S > 1 && tasks > kMinFillSlots * (double)slots) return sb;
   }
   return 0;
 }
 
-// Quarter rows: a launch with a little more than one (sequence, kv head)
-// row per CU (1.0-1.3) on the 16-bit kernels at D = 128 cuts rows into
-// quarters of the table width (16+ blocks), whatever their lengths. With
-// whole rows the rows past one per CU land as second workgroups on CUs that
-// already stream one, and those CUs take about twice as long as the rest.
-// Measured on MI355X (bf16, HIP graph replay, three workgroups per CU):
-// 8 / 1 heads at 272 and 320 rows of 4096 tokens 136.4 / 139.9 us whole
-// against 104.2 / 113.6 us in quarters (rows of U[1024, 4096]: 87.0 / 92.8
-// -> 67.0 / 81.0 us; of 2048 tokens: 70.1 / 72.3 -> 54.7 / 61.4 us); MHA
-// (VALU kernel) at 288 and 320 rows of 4096 tokens 121.6 / 123.0 -> 100.2 /
-// 109.2 us, of U[1024, 4096] 76.7 / 76.8 -> 71.9 / 73.4 us. At exactly one
-// row per CU and from about 1.5 on, whole rows do as well or better; at
-// D = 64 the quarters lose on some length mixes, so the rule stays at D = 128.
-// Past two rows per CU (2.0-2.6) the same holds for rows of equal length
-// only: the two-per-CU cap then leaves a second round of whole rows, and
-// half rows gain (8 / 1 heads, 528-640 rows of 4096 tokens: 216.1 / 264.9 /
-// 278.0 -> 196.3 / 205.8 / 210.1 us; MHA on the VALU kernel +2 to +7 %),
-// while rows of mixed length balance by themselves and lose 3-11 % split.
-// So half rows need the caller's token total to show the rows full (mean
-// fill of the table 0.8 or more; fill = 0: unknown).
+// Quarter and half rows (kRowCuts) on the 16-bit VALU and matrix-core
+// kernels: the task size (a power of two >= 16 tiles, at most the table
+// width over the window's parts) of the first window that holds, or 0.
 int32_t quarter_row_blocks(int32_t n, int32_t kv_tasks, int32_t D, bool f32, bool mfma,
                            int cus, int32_t wt, double fill) {
   const int64_t rows = (int64_t)n * kv_tasks;
   if (f32 || mfma || cus <= 0 || wt < 4 * kMinFillBlocks) return 0;
-  // D = 64 only for rows the total shows all but equal: near-full rows of
-  // mixed length (mean fill 0.8-0.9) lost up to 20 % there, equal ones gained
-  // 10-20 %
-  if (D != 128 && !(D == 64 && fill >= kFullRowsD64)) return 0;
-  int32_t parts = 0;
-  if (rows > cus && rows * 10 <= (int64_t)cus * 13)
-    parts = 4;
-  else if (fill >= kMaxFillRows && rows > 2 * (int64_t)cus && rows * 10 <= (int64_t)cus * 26)
-    parts = 2;
-  if (parts == 0) return 0;
-  int32_t q = kMinFillBlocks;
-  while (q * 2 <= wt / parts) q *= 2;
-  return q;
+  for (const RowCut& c : kRowCuts) {
+    if (c.head_size != D || fill < c.fill_lo || rows * 10 <= (int64_t)c.lo10 * cus ||
+        rows * 10 > (int64_t)c.hi10 * cus)
+      continue;
+    int32_t q = kMinFillBlocks;
+    while (q * 2 <= wt / c.parts) q *= 2;
+    return q;
+  }
+  return 0;
 }
 
 }  // namespace
@@ -510,11 +535,7 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   const int32_t kv_tasks = KVH * sp.passes;
   const int elt = f32 ? 4 : 2;
   bool filled = false;
-  if (sb <= 0 && fill > 0.0 && fill < kMaxFillRows && sp.mm && sp.kernel_g == 16 && cus > 0 &&
-      2 * (int64_t)n * kv_tasks <= 3 * (int64_t)cus) {
-    // uneven rows on the one-column-group matrix-core kernel, up to 1.5 rows
-    // per CU (with more, they balance by themselves: -3 to -6 % split at two
-    // rows per CU, rows of 2048 tokens): the slot fill
+  if (sb <= 0 && slot_fill_window(sp, (int64_t)n * kv_tasks, cus, fill)) {
     sb = fill_split_blocks(n, kv_tasks, wt, (int64_t)kFillPerCu * cus, fill);
     filled = sb > 0;
   }
