@@ -460,23 +460,28 @@ __device__ __forceinline__ void finish_task(const TiledParams& p, const Task& t,
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.f;
+    // every lane reads its chunk's slice of every wave's state at once (lanes
+    // past LPT repeat a chunk's reads and store nothing): the LDS reads issue
+    // together instead of one wave's after another's
+    float4 sa[kWavesPerTask], sb[kWavesPerTask];
+#pragma unroll
+    for (int w = 0; w < kWavesPerTask; ++w) {
+      const float4* src = reinterpret_cast<const float4*>(&ws.acc[w][g][chunk * 8]);
+      sa[w] = src[0];
+      sb[w] = src[1];
+    }
 #pragma unroll
     for (int w = 0; w < kWavesPerTask; ++w) {
       const float sc = fast_exp2(ws.m[w][g] - Ms);  // 0 for a wave without blocks
       lt += sc * ws.l[w][g];
-      if (lane < LPT) {
-        const float4* src = reinterpret_cast<const float4*>(&ws.acc[w][g][chunk * 8]);
-        const float4 a = src[0];
-        const float4 b = src[1];
-        o[0] += sc * a.x;
-        o[1] += sc * a.y;
-        o[2] += sc * a.z;
-        o[3] += sc * a.w;
-        o[4] += sc * b.x;
-        o[5] += sc * b.y;
-        o[6] += sc * b.z;
-        o[7] += sc * b.w;
-      }
+      o[0] += sc * sa[w].x;
+      o[1] += sc * sa[w].y;
+      o[2] += sc * sa[w].z;
+      o[3] += sc * sa[w].w;
+      o[4] += sc * sb[w].x;
+      o[5] += sc * sb[w].y;
+      o[6] += sc * sb[w].z;
+      o[7] += sc * sb[w].w;
     }
     const float inv = 1.f / lt;
 #pragma unroll
