@@ -73,7 +73,7 @@ def run_simulation(steps: int = 300, seed: int = 4, device=None, G: int = 256, C
                    H: int = 32, KVH: int = 32, D: int = 128, BS: int = 16,
                    dtype: torch.dtype = torch.float16, arrivals: float = 4.0,
                    prompt: tuple[int, int] = (64, 512), output: tuple[int, int] = (32, 512),
-                   tol: float = 3e-3, oracle_every: int = 10, fused: bool = True,
+                   tol: float = 2e-3, oracle_every: int = 10, fused: bool = True,
                    planner: str = "host", cpu_fraction: float = 0.0) -> dict:
     dev = device or torch.device("cuda", 0)
     rng = random.Random(seed)

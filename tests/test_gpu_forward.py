@@ -226,8 +226,8 @@ def test_continuous_batching_simulation(gpu, fused, planner, cpu_fraction):
         assert stats["device_planned_steps"] > 250
     else:
         assert stats["split_steps"] > 100
-    assert stats["max_err_vs_mono"] <= 3e-3
-    assert stats["max_err_vs_f64"] <= 3e-3
+    assert stats["max_err_vs_mono"] <= 2e-3
+    assert stats["max_err_vs_f64"] <= 2e-3
 
 
 @pytest.mark.parametrize("planner,cpu_fraction", [("host", 0.0), ("device", 0.0), ("host", "auto")])
@@ -243,8 +243,8 @@ def test_continuous_batching_simulation_32_token_blocks(gpu, planner, cpu_fracti
     assert stats["failures"] == [], stats["failures"][:5]
     assert stats["rows_vs_f64"] >= stats["decode_rows"] // 20  # every row of every 10th step
     assert stats["decode_rows"] > 300
-    assert stats["max_err_vs_mono"] <= 3e-3
-    assert stats["max_err_vs_f64"] <= 3e-3
+    assert stats["max_err_vs_mono"] <= 2e-3
+    assert stats["max_err_vs_f64"] <= 2e-3
 
 
 @pytest.mark.parametrize("H,KVH,dtype", [(32, 8, torch.bfloat16), (40, 8, torch.float16)])
@@ -254,7 +254,7 @@ def test_continuous_batching_simulation_grouped_heads(gpu, H, KVH, dtype, cpu_fr
     group), through the fused launch and the hybrid split."""
     from tests.simulate import run_simulation
 
-    tol = 3e-3 if dtype == torch.float16 else 1.6e-2  # 16-bit output of the split path
+    tol = 2e-3 if dtype == torch.float16 else 1.6e-2  # 16-bit output of the split path
     stats = run_simulation(steps=120, seed=11, device=gpu, H=H, KVH=KVH, dtype=dtype,
                            cpu_fraction=cpu_fraction, tol=tol)
     print({k: v for k, v in stats.items() if k != "failures"})
