@@ -140,6 +140,31 @@ def test_host_decode_thread_counts_bit_identical(isa):
     assert _lib.load_lib().fd_host_decode_threads() >= 1
 
 
+@pytest.mark.parametrize("H,KVH", [(32, 32), (12, 6), (32, 8)])
+def test_host_decode_head_groups_bit_identical(H, KVH, isa):
+    """A work item covers a group of adjacent kv heads of one row, the more
+    the fewer workers there are (9 rows: every kv head at 1 thread, down to
+    one kv head at 64), with a shorter last group when the group size does not
+    divide KVH. Every grouping gives the same bits and the oracle's values,
+    and a row with a block id outside the cache is NaN in every head."""
+    n, D, BS, C = 9, 64, 16, 120
+    q, kc, vc, bt, lens = cases.rand_case(n, H, KVH, D, BS, C, torch.float16, 200, KVH)
+    lens[2] = 0
+    lens[5] = max(int(lens[5]), 40)
+    bad = bt.clone()
+    bad[5, 1] = C + 3
+    base = run(q, kc, vc, bad, lens, 0.125, torch.float32, threads=1)
+    for t in (2, 3, 4, 8, 16, 64):
+        o, l = run(q, kc, vc, bad, lens, 0.125, torch.float32, threads=t)
+        assert torch.equal(o.nan_to_num(9.0), base[0].nan_to_num(9.0)), t
+        assert torch.equal(l.nan_to_num(9.0), base[1].nan_to_num(9.0)), t
+    ok = torch.ones(n, dtype=torch.bool)
+    ok[5] = False
+    assert torch.isnan(base[0][5]).all() and torch.isnan(base[1][:, 5]).all()
+    ref_out, ref_lse = oracle.decode_attn_host_layout_f64(q[ok], kc, vc, bt[ok], lens[ok], 0.125)
+    check(base[0][ok], base[1][:, ok], ref_out, ref_lse, lens[ok], torch.float16)
+
+
 def test_host_decode_strided_views_and_padded_table(isa):
     """q and out as head-major views, the table padded with junk past each
     row's blocks (never read), the caches as halves of one buffer."""

@@ -6,7 +6,7 @@
 // elements, exp2). No include guard on purpose.
 //
 // Needs, from the including namespace: V, HostArgs, Scratch, load1,
-// f32_to_bf16, kPrefetchBlocks.
+// f32_to_bf16.
 
 // acc[g][d0 .. d0 + W*CU) = acc * alpha[g] + sum_t s[g][t] * V[t][...] for as
 // many whole groups of CU chunks as fit below DW, advancing d; the rest goes
@@ -209,11 +209,19 @@ __attribute__((always_inline)) inline void score_tokens(const char* kp, int64_t 
   }
 }
 
-// Online-softmax partial of query heads kh*Gr + g0 .. + G-1 (Gr = H / KVH) of
-// sequence i over kv head kh. Returns false if the row is invalid (a length
-// past its table or a block id outside the cache).
+// Online-softmax partials of query heads g0 .. g0 + G - 1 of each of the kv
+// heads kh0 .. kh0 + nkh - 1 (query head kh * Gr + g0 + g, Gr = H / KVH) of
+// sequence i. Blocks are the outer loop and the item's kv heads the inner
+// one: in the host tier's [C, KVH, BS, D] layout the runs of adjacent kv heads
+// of a block are adjacent, so one item streams nkh * BS * D elements of K and
+// of V per block in one piece instead of one head's run (measured on the
+// host tier of the vicuna-7b split: a plain read of 4 KiB runs per block
+// reaches ~80 % of the cores' rate for whole blocks). Each (block, kv head)
+// step is one online-softmax step of that head's G query heads. Returns false
+// if the row is invalid (a length past its table or a block id outside the
+// cache).
 template <int DT, int G>
-bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
+bool run_heads(const HostArgs& a, int i, int kh0, int nkh, int g0, Scratch& w) {
   using T = typename V::T;
   constexpr int W = V::W;
   constexpr int elt = DT == FD_F32 ? 4 : 2;
@@ -230,30 +238,30 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
   const int L = a.lens[i];
   const int nb = (L + BS - 1) / BS;
   if (nb > a.bt_width) return false;
-  w.q.resize((size_t)G * D);
-  w.acc.assign((size_t)G * D, 0.f);
+  const int GH = nkh * G;  // query heads of the item
+  w.q.resize((size_t)GH * D);
+  w.acc.assign((size_t)GH * D, 0.f);
   w.s.resize((size_t)G * BS);
-  float* qf = w.q.data();
-  float* acc = w.acc.data();
+  w.m.assign((size_t)GH, -INFINITY);
+  w.l.assign((size_t)GH, 0.f);
   float* s = w.s.data();
   const float qs = a.scale * 1.4426950408889634f;  // scores in the log2 domain
-  for (int g = 0; g < G; ++g) {
-    const int64_t qb = (int64_t)i * a.q_ss + (int64_t)(kh * Gr + g0 + g) * a.q_sh;
-    for (int d = 0; d < D; ++d) qf[g * D + d] = load1(a.q, qb + d, a.dt) * qs;
-  }
-  const uint16_t* qh = nullptr;  // the raw bf16 q rows, for the pair dot products
-  if constexpr (V::kBf16Dot && DT == FD_BF16) {
-    w.qh.resize((size_t)G * D);
+  for (int j = 0; j < nkh; ++j)
     for (int g = 0; g < G; ++g) {
-      const int64_t qb = (int64_t)i * a.q_ss + (int64_t)(kh * Gr + g0 + g) * a.q_sh;
-      memcpy(w.qh.data() + (size_t)g * D, static_cast<const uint16_t*>(a.q) + qb, (size_t)D * 2);
+      const int64_t qb = (int64_t)i * a.q_ss + (int64_t)((kh0 + j) * Gr + g0 + g) * a.q_sh;
+      float* qd = w.q.data() + (size_t)(j * G + g) * D;
+      for (int d = 0; d < D; ++d) qd[d] = load1(a.q, qb + d, a.dt) * qs;
     }
-    qh = w.qh.data();
-  }
-  float m[G], l[G], alpha[G];
-  for (int g = 0; g < G; ++g) {
-    m[g] = -INFINITY;
-    l[g] = 0.f;
+  const uint16_t* qh_all = nullptr;  // the raw bf16 q rows, for the pair dot products
+  if constexpr (V::kBf16Dot && DT == FD_BF16) {
+    w.qh.resize((size_t)GH * D);
+    for (int j = 0; j < nkh; ++j)
+      for (int g = 0; g < G; ++g) {
+        const int64_t qb = (int64_t)i * a.q_ss + (int64_t)((kh0 + j) * Gr + g0 + g) * a.q_sh;
+        memcpy(w.qh.data() + (size_t)(j * G + g) * D, static_cast<const uint16_t*>(a.q) + qb,
+               (size_t)D * 2);
+      }
+    qh_all = w.qh.data();
   }
   const char* kbase = static_cast<const char*>(a.k);
   const char* vbase = static_cast<const char*>(a.v);
@@ -262,129 +270,147 @@ bool run_heads(const HostArgs& a, int i, int kh, int g0, Scratch& w) {
     const int64_t bid = row_bt[b];
     if (bid < 0 || bid >= a.num_blocks) return false;
     const int ntok = std::min(BS, L - b * BS);
-    const int64_t base = bid * a.sb + (int64_t)kh * a.sh;
-    int64_t nbase = -1;  // a later block's rows, prefetched a few at a time below
-    if (b + kPrefetchBlocks < nb) {
-      const int64_t nid = row_bt[b + kPrefetchBlocks];
-      if (nid >= 0 && nid < a.num_blocks) nbase = nid * a.sb + (int64_t)kh * a.sh;
+    // the next block's id, for the prefetch after the item's last kv head
+    int64_t next_bid = -1;
+    if (b + 1 < nb) {
+      const int64_t nid = row_bt[b + 1];
+      if (nid >= 0 && nid < a.num_blocks) next_bid = nid;
     }
-    int pf = 0;  // next row of that block to prefetch
-    auto prefetch_rows = [&](int upto) {
-      if (nbase < 0) return;
-      for (; pf < upto && pf < BS; ++pf)
-        for (int off = 0; off < D * elt; off += 64) {
-          _mm_prefetch(kbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
-          _mm_prefetch(vbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
+    for (int j = 0; j < nkh; ++j) {
+      const int kh = kh0 + j;
+      const int64_t base = bid * a.sb + (int64_t)kh * a.sh;
+      // the run read after this one, prefetched a few rows at a time below:
+      // the next kv head's run of this block, else the next block's first
+      const int64_t nbase = j + 1 < nkh    ? base + a.sh
+                            : next_bid >= 0 ? next_bid * a.sb + (int64_t)kh0 * a.sh
+                                            : -1;
+      int pf = 0;  // next row of that run to prefetch
+      auto prefetch_rows = [&](int upto) {
+        if (nbase < 0) return;
+        for (; pf < upto && pf < BS; ++pf)
+          for (int off = 0; off < D * elt; off += 64) {
+            _mm_prefetch(kbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
+            _mm_prefetch(vbase + (nbase + (int64_t)pf * a.st) * elt + off, _MM_HINT_T0);
+          }
+      };
+      const float* qf = w.q.data() + (size_t)j * G * D;
+      const uint16_t* qh = qh_all != nullptr ? qh_all + (size_t)j * G * D : nullptr;
+      float* acc = w.acc.data() + (size_t)j * G * D;
+      float* mj = w.m.data() + j * G;
+      float* lj = w.l.data() + j * G;
+      float alpha[G];
+      // scores, TT tokens at a time where the accumulators fit
+      int t0 = 0;
+      if constexpr (TT >= 2) {
+        for (; t0 + TT <= ntok; t0 += TT) {
+          // half the next run's rows over the score loop, the rest below:
+          // measured best on Zen 5 against TT rows per group or one per group
+          prefetch_rows(pf + (TT + 1) / 2);
+          score_tokens<DT, G, TT>(kbase + (base + (int64_t)t0 * a.st) * elt, a.st * elt, qf, qh,
+                                  qs, D, DW, s + t0, BS);
         }
-    };
-    // scores, TT tokens at a time where the accumulators fit
-    int t0 = 0;
-    if constexpr (TT >= 2) {
-      for (; t0 + TT <= ntok; t0 += TT) {
-        // half the next block's rows over the score loop, the rest below:
-        // measured best on Zen 5 against TT rows per group or one per group
-        prefetch_rows(pf + (TT + 1) / 2);
-        score_tokens<DT, G, TT>(kbase + (base + (int64_t)t0 * a.st) * elt, a.st * elt, qf, qh,
-                                qs, D, DW, s + t0, BS);
       }
-    }
-    prefetch_rows(BS);
-    for (int t = t0; t < ntok; ++t)
-      score_token<DT, G, U>(kbase + (base + (int64_t)t * a.st) * elt, qf, qh, qs, D, DW, s + t,
-                            BS);
-    // one online-softmax step per head
-    for (int g = 0; g < G; ++g) {
-      float* sg = s + g * BS;
-      float bmax = -INFINITY;
-      {
-        int t = 0;
-        if (ntok >= W) {
-          T mx = V::load(sg);
-          for (t = W; t + W <= ntok; t += W) mx = V::max(mx, V::load(sg + t));
-          bmax = V::hmax(mx);
-        }
-        for (; t < ntok; ++t) bmax = std::max(bmax, sg[t]);
-      }
-      const float mn = std::max(m[g], bmax);
-      alpha[g] = m[g] == -INFINITY ? 0.f : V::exp2_1(m[g] - mn);
-      const T mv = V::set1(mn);
-      T ps = V::zero();
-      int t = 0;
-      for (; t + W <= ntok; t += W) {
-        const T p = V::exp2(V::sub(V::load(sg + t), mv));
-        V::store(sg + t, p);
-        ps = V::add(ps, p);
-      }
-      float psum = V::hsum(ps);
-      for (; t < ntok; ++t) {
-        sg[t] = V::exp2_1(sg[t] - mn);
-        psum += sg[t];
-      }
-      l[g] = l[g] * alpha[g] + psum;
-      m[g] = mn;
-    }
-    // acc = acc * alpha + P.V, CU chunks of W columns at a time, then
-    // halving groups for what is left
-    const char* vb = vbase + base * elt;
-    int d = 0;
-    if (perm)
-      pv_groups<DT, G, CU, true>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
-    else
-      pv_groups<DT, G, CU>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
-    for (; d < D; ++d)
+      prefetch_rows(BS);
+      for (int t = t0; t < ntok; ++t)
+        score_token<DT, G, U>(kbase + (base + (int64_t)t * a.st) * elt, qf, qh, qs, D, DW,
+                              s + t, BS);
+      // one online-softmax step per head
       for (int g = 0; g < G; ++g) {
-        float x = acc[g * D + d] * alpha[g];
-        for (int t = 0; t < ntok; ++t) x += s[g * BS + t] * load1(vb, (int64_t)t * a.st + d, DT);
-        acc[g * D + d] = x;
-      }
-  }
-  for (int g = 0; g < G; ++g) {
-    const int h = kh * Gr + g0 + g;
-    const float inv = 1.f / l[g];
-    float* o = acc + g * D;
-    if (perm) {  // back from the even / odd layout of each 2W span
-      float tmp[2 * W];
-      for (int d0 = 0; d0 < D; d0 += 2 * W) {
-        for (int j = 0; j < W; ++j) {
-          tmp[2 * j] = o[d0 + j];
-          tmp[2 * j + 1] = o[d0 + W + j];
+        float* sg = s + g * BS;
+        float bmax = -INFINITY;
+        {
+          int t = 0;
+          if (ntok >= W) {
+            T mx = V::load(sg);
+            for (t = W; t + W <= ntok; t += W) mx = V::max(mx, V::load(sg + t));
+            bmax = V::hmax(mx);
+          }
+          for (; t < ntok; ++t) bmax = std::max(bmax, sg[t]);
         }
-        memcpy(o + d0, tmp, sizeof(tmp));
+        const float mn = std::max(mj[g], bmax);
+        alpha[g] = mj[g] == -INFINITY ? 0.f : V::exp2_1(mj[g] - mn);
+        const T mv = V::set1(mn);
+        T ps = V::zero();
+        int t = 0;
+        for (; t + W <= ntok; t += W) {
+          const T p = V::exp2(V::sub(V::load(sg + t), mv));
+          V::store(sg + t, p);
+          ps = V::add(ps, p);
+        }
+        float psum = V::hsum(ps);
+        for (; t < ntok; ++t) {
+          sg[t] = V::exp2_1(sg[t] - mn);
+          psum += sg[t];
+        }
+        lj[g] = lj[g] * alpha[g] + psum;
+        mj[g] = mn;
       }
-    }
-    for (int d = 0; d < D; ++d) o[d] *= inv;
-    const int64_t ob = (int64_t)i * a.out_ss + (int64_t)h * a.out_sh;
-    if (a.out_dt == FD_F32) {
-      memcpy(static_cast<float*>(a.out) + ob, o, (size_t)D * 4);
-    } else if (a.out_dt == FD_F16) {
-      uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
+      // acc = acc * alpha + P.V, CU chunks of W columns at a time, then
+      // halving groups for what is left
+      const char* vb = vbase + base * elt;
       int d = 0;
-      for (; d + 8 <= D; d += 8)
-        _mm_storeu_si128(reinterpret_cast<__m128i*>(dst + d),
-                         _mm256_cvtps_ph(_mm256_loadu_ps(o + d), _MM_FROUND_TO_NEAREST_INT));
-      for (; d < D; ++d) dst[d] = _cvtss_sh(o[d], _MM_FROUND_TO_NEAREST_INT);
-    } else {
-      uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
-      for (int d = 0; d < D; ++d) dst[d] = f32_to_bf16(o[d]);
+      if (perm)
+        pv_groups<DT, G, CU, true>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
+      else
+        pv_groups<DT, G, CU>(acc, s, alpha, vb, a.st, D, DW, BS, ntok, d);
+      for (; d < D; ++d)
+        for (int g = 0; g < G; ++g) {
+          float x = acc[g * D + d] * alpha[g];
+          for (int t = 0; t < ntok; ++t) x += s[g * BS + t] * load1(vb, (int64_t)t * a.st + d, DT);
+          acc[g * D + d] = x;
+        }
     }
-    a.lse[(int64_t)h * a.lse_sh + i] = (m[g] + std::log2(l[g])) * 0.6931471805599453f;
   }
+  for (int j = 0; j < nkh; ++j)
+    for (int g = 0; g < G; ++g) {
+      const int h = (kh0 + j) * Gr + g0 + g;
+      const float lh = w.l[j * G + g];
+      const float inv = 1.f / lh;
+      float* o = w.acc.data() + (size_t)(j * G + g) * D;
+      if (perm) {  // back from the even / odd layout of each 2W span
+        float tmp[2 * W];
+        for (int d0 = 0; d0 < D; d0 += 2 * W) {
+          for (int e = 0; e < W; ++e) {
+            tmp[2 * e] = o[d0 + e];
+            tmp[2 * e + 1] = o[d0 + W + e];
+          }
+          memcpy(o + d0, tmp, sizeof(tmp));
+        }
+      }
+      for (int d = 0; d < D; ++d) o[d] *= inv;
+      const int64_t ob = (int64_t)i * a.out_ss + (int64_t)h * a.out_sh;
+      if (a.out_dt == FD_F32) {
+        memcpy(static_cast<float*>(a.out) + ob, o, (size_t)D * 4);
+      } else if (a.out_dt == FD_F16) {
+        uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
+        int d = 0;
+        for (; d + 8 <= D; d += 8)
+          _mm_storeu_si128(reinterpret_cast<__m128i*>(dst + d),
+                           _mm256_cvtps_ph(_mm256_loadu_ps(o + d), _MM_FROUND_TO_NEAREST_INT));
+        for (; d < D; ++d) dst[d] = _cvtss_sh(o[d], _MM_FROUND_TO_NEAREST_INT);
+      } else {
+        uint16_t* dst = static_cast<uint16_t*>(a.out) + ob;
+        for (int d = 0; d < D; ++d) dst[d] = f32_to_bf16(o[d]);
+      }
+      a.lse[(int64_t)h * a.lse_sh + i] = (w.m[j * G + g] + std::log2(lh)) * 0.6931471805599453f;
+    }
   return true;
 }
 
 template <int DT>
-bool run_heads_dt(const HostArgs& a, int i, int kh, int g0, int G, Scratch& w) {
+bool run_heads_dt(const HostArgs& a, int i, int kh0, int nkh, int g0, int G, Scratch& w) {
   switch (G) {
-    case 1: return run_heads<DT, 1>(a, i, kh, g0, w);
-    case 2: return run_heads<DT, 2>(a, i, kh, g0, w);
-    case 4: return run_heads<DT, 4>(a, i, kh, g0, w);
-    default: return run_heads<DT, 8>(a, i, kh, g0, w);
+    case 1: return run_heads<DT, 1>(a, i, kh0, nkh, g0, w);
+    case 2: return run_heads<DT, 2>(a, i, kh0, nkh, g0, w);
+    case 4: return run_heads<DT, 4>(a, i, kh0, nkh, g0, w);
+    default: return run_heads<DT, 8>(a, i, kh0, nkh, g0, w);
   }
 }
 
-// Query heads g0 .. g0 + G - 1 (G in {1, 2, 4, 8}) of (sequence i, kv head kh).
-bool run_group(const HostArgs& a, int i, int kh, int g0, int G, Scratch& w) {
-  if (a.dt == FD_F16) return run_heads_dt<FD_F16>(a, i, kh, g0, G, w);
-  if (a.dt == FD_BF16) return run_heads_dt<FD_BF16>(a, i, kh, g0, G, w);
-  return run_heads_dt<FD_F32>(a, i, kh, g0, G, w);
+// Query heads g0 .. g0 + G - 1 (G in {1, 2, 4, 8}) of each kv head kh0 ..
+// kh0 + nkh - 1 of sequence i.
+bool run_group(const HostArgs& a, int i, int kh0, int nkh, int g0, int G, Scratch& w) {
+  if (a.dt == FD_F16) return run_heads_dt<FD_F16>(a, i, kh0, nkh, g0, G, w);
+  if (a.dt == FD_BF16) return run_heads_dt<FD_BF16>(a, i, kh0, nkh, g0, G, w);
+  return run_heads_dt<FD_F32>(a, i, kh0, nkh, g0, G, w);
 }
