@@ -100,7 +100,7 @@ def test_share_tuner_bounds_and_backend_validation():
     assert t.update(False) == 1.0
     with pytest.raises(ValueError):
         ShareTuner(start=2.0)
-    assert backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction="auto")._host_share() == 0.75
+    assert backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction="auto")._host_share() == 0.85
     assert backend.SplitDecodeImpl(4, 4, 64, 0.1, cpu_fraction=0.3)._host_share() == 0.3
     for bad in (1.5, -0.1, "fast"):
         with pytest.raises(ValueError):
