@@ -147,7 +147,7 @@ def test_backend_uses_the_hybrid_only_above_its_host_bytes_threshold(gpu, monkey
         torch.cuda.synchronize()
         assert (len(calls) == 1) == expect_hybrid
         if expect_hybrid:
-            assert calls[0] == 0.75  # the tuner's starting share
+            assert calls[0] == plan.ShareTuner().fraction  # the tuner's starting share
         assert float((out.double().cpu() - sc.ref).abs().max()) <= TOL[dtype]
     state.STORE = None
 
