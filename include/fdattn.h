@@ -453,6 +453,40 @@ int fd_host_decode_partial(
     float* lse, int64_t lse_stride_head,
     int32_t num_threads);
 
+/* fd_host_decode_partial in the background: checks the arguments as
+ * fd_host_decode_partial does (an invalid call returns its error here and
+ * queues nothing), queues the call for a runner thread of the library and
+ * returns at once with *call, an id for fd_host_decode_wait. The runner first
+ * waits for ready_event (a hipEvent_t; NULL: none), e.g. one recorded behind
+ * the copy of q to the host, then makes the call; queued calls run one at a
+ * time in queue order. Every buffer must stay valid, and out / lse unread,
+ * until fd_host_decode_wait(*call) has returned; every started call must be
+ * waited for once. No counterpart in the reference, whose host-tier kernel
+ * runs synchronously inside the forward (fastdecode/backend.py:343-351); for
+ * callers that overlap the host cores' share with the GPU's work (the hybrid
+ * split) without a thread of their own. */
+int fd_host_decode_partial_start(
+    void* ready_event,
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    int32_t num_threads, int64_t* call);
+
+/* Blocks until the call queued as `call` has run and returns its status (the
+ * message of a failure for fd_last_error() on this thread). *seconds (may be
+ * NULL) = the time the call itself took, from the end of the wait for its
+ * event. An id that is not pending (never started, or already waited for)
+ * is FD_ERR_INVALID. */
+int fd_host_decode_wait(int64_t call, double* seconds);
+
 /* Worker count fd_host_decode_partial uses when num_threads is 0: the count
  * set by fd_host_set_threads, else FASTDECODE_CPU_THREADS, else one per CPU
  * of the process's affinity mask. Replaces the extension's get_num_threads

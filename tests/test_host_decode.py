@@ -283,3 +283,91 @@ def test_host_stream_read_checksum_and_arguments():
     assert lib.fd_host_stream_read(buf.data_ptr(), 64, 1 << 20, ctypes.byref(out)) == \
         _lib.FD_ERR_INVALID
     assert lib.fd_host_stream_read(None, 0, 1, ctypes.byref(out)) == _lib.FD_OK and out.value == 0
+
+
+def test_host_decode_start_matches_the_synchronous_call(isa):
+    """fd_host_decode_partial_start / fd_host_decode_wait: queued calls run in
+    order on the library's runner thread and give the synchronous call's bits;
+    the wait returns the call's own time."""
+    cases_ = [cases.rand_case(9, 8, 2, 128, 16, 80, torch.float16, 300, s) for s in (1, 2, 3)]
+    want = [run(*c[:5], 0.1, torch.float32) for c in cases_]
+    outs, calls = [], []
+    for c in cases_:
+        q, kc, vc, bt, lens = c
+        out = torch.full((9, 8, 128), 7.0)
+        lse = torch.full((8, 9), 7.0)
+        calls.append(ops.host_decode_start(q, kc, vc, bt, lens, 0.1, out, lse))
+        outs.append((out, lse))
+    for call, (out, lse), (wo, wl) in zip(calls, outs, want):
+        assert call.wait() >= 0.0
+        assert torch.equal(out, wo) and torch.equal(lse, wl)
+    assert calls[0].wait() == 0.0  # a second wait of the Python handle is a no-op
+
+
+def test_host_decode_start_checks_before_queueing():
+    """Bad arguments are refused at start (nothing queued); an id that is not
+    pending is refused by the wait; a call's range errors still give NaN rows."""
+    lib = _lib.load_lib()
+    q, kc, vc, bt, lens = cases.rand_case(2, 4, 2, 64, 16, 8, torch.float16, 30, 0)
+    out = torch.empty(2, 4, 64)
+    lse = torch.empty(4, 2)
+    call = ctypes.c_int64(-1)
+    st = lib.fd_host_decode_partial_start(
+        None, q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+        kc.stride(0), kc.stride(1), kc.stride(2), 8, bt.data_ptr(), bt.stride(0), bt.shape[1],
+        lens.data_ptr(), 2, 3, 2, 64, 16, 0.1, _lib.FD_F16, out.data_ptr(), out.stride(0),
+        out.stride(1), _lib.FD_F32, lse.data_ptr(), 2, 0, ctypes.byref(call))
+    assert st == _lib.FD_ERR_INVALID and b"bad sizes" in lib.fd_last_error()
+    assert call.value == -1
+    with pytest.raises(RuntimeError, match="share a dtype"):
+        ops.host_decode_start(q.float(), kc, vc, bt, lens, 0.1, out, lse)
+    secs = ctypes.c_double()
+    assert lib.fd_host_decode_wait(10**12, ctypes.byref(secs)) == _lib.FD_ERR_INVALID
+    assert b"no pending call" in lib.fd_last_error()
+    st = lib.fd_host_decode_partial_start(
+        None, q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(),
+        kc.stride(0), kc.stride(1), kc.stride(2), 8, bt.data_ptr(), bt.stride(0), bt.shape[1],
+        lens.data_ptr(), 2, 4, 2, 64, 16, 0.1, _lib.FD_F16, out.data_ptr(), out.stride(0),
+        out.stride(1), _lib.FD_F32, lse.data_ptr(), 2, 0, ctypes.byref(call))
+    assert st == _lib.FD_OK and call.value > 0
+    assert lib.fd_host_decode_wait(call.value, None) == _lib.FD_OK
+    assert lib.fd_host_decode_wait(call.value, None) == _lib.FD_ERR_INVALID  # waited already
+    bad = bt.clone()
+    bad[1, 0] = 8 + 5
+    o2, l2 = torch.empty(2, 4, 64), torch.empty(4, 2)
+    ops.host_decode_start(q, kc, vc, bad, lens, 0.1, o2, l2).wait()
+    assert torch.isnan(o2[1]).all() and torch.isnan(l2[:, 1]).all()
+    assert torch.isfinite(o2[0]).all()
+
+
+def _child_start(conn, args):
+    q, kc, vc, bt, lens = args
+    out = torch.empty(q.shape, dtype=torch.float32)
+    lse = torch.empty(q.shape[1], q.shape[0])
+    ops.host_decode_start(q, kc, vc, bt, lens, 0.1, out, lse, num_threads=4).wait()
+    conn.send((out.numpy().copy(), lse.numpy().copy()))
+    conn.close()
+
+
+def test_host_decode_start_in_a_forked_child():
+    """A child forked after the parent used the runner thread gets its own."""
+    import multiprocessing as mp
+
+    args = cases.rand_case(11, 8, 2, 64, 16, 60, torch.float16, 150, 5)
+    out = torch.empty(11, 8, 64)
+    lse = torch.empty(8, 11)
+    ops.host_decode_start(*args, 0.1, out, lse, num_threads=4).wait()
+    ctx = mp.get_context("fork")
+    rd, wr = ctx.Pipe(duplex=False)
+    proc = ctx.Process(target=_child_start, args=(wr, args))
+    proc.start()
+    wr.close()
+    try:
+        assert rd.poll(120), "forked child did not answer"
+        child = tuple(torch.from_numpy(x) for x in rd.recv())
+    finally:
+        proc.join(30)
+        if proc.is_alive():
+            proc.kill()
+    assert proc.exitcode == 0
+    assert torch.equal(child[0], out) and torch.equal(child[1], lse)

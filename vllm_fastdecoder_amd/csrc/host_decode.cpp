@@ -47,6 +47,7 @@
 
 #include "../../include/fdattn.h"
 #include "fd_errors.h"
+#include "host_decode.h"
 
 namespace fd {
 namespace {
@@ -591,14 +592,15 @@ extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_th
   return FD_OK;
 }
 
-extern "C" int fd_host_decode_partial(
-    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
-    const void* v_cache, int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
-    int64_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
-    const int32_t* lens, int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
-    int32_t block_size, float scale, int32_t kv_dtype, void* out, int64_t out_stride_seq,
-    int64_t out_stride_head, int32_t out_dtype, float* lse, int64_t lse_stride_head,
-    int32_t num_threads) {
+namespace fd {
+
+// fd_host_decode_partial's argument checks (shared with the background form
+// in host_async.hip, which checks before it queues a call).
+int host_decode_check(const void* q, const void* k_cache, const void* v_cache, int64_t num_blocks,
+                      const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+                      const int32_t* lens, int32_t n, int32_t num_heads, int32_t num_kv_heads,
+                      int32_t head_size, int32_t block_size, float scale, int32_t kv_dtype,
+                      void* out, int32_t out_dtype, float* lse, int32_t num_threads) {
   if (n < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
       head_size <= 0 || head_size > 1024 || block_size <= 0 || block_size > 1024 ||
       bt_width < 0 || num_blocks < 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
@@ -615,9 +617,26 @@ extern "C" int fd_host_decode_partial(
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: NULL pointer");
   if (bt_width > 0 && bt_stride < bt_width)
     return set_error(FD_ERR_INVALID, "fd_host_decode_partial: bt_stride < bt_width");
-  int bits = isa_bits();
-  if (bits == 0)
+  if (isa_bits() == 0)
     return set_error(FD_ERR_UNSUPPORTED, "fd_host_decode_partial: the CPU lacks AVX2/FMA/F16C");
+  return FD_OK;
+}
+
+}  // namespace fd
+
+extern "C" int fd_host_decode_partial(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens, int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype, void* out, int64_t out_stride_seq,
+    int64_t out_stride_head, int32_t out_dtype, float* lse, int64_t lse_stride_head,
+    int32_t num_threads) {
+  const int rc = host_decode_check(q, k_cache, v_cache, num_blocks, block_table, bt_stride,
+                                   bt_width, lens, n, num_heads, num_kv_heads, head_size,
+                                   block_size, scale, kv_dtype, out, out_dtype, lse, num_threads);
+  if (rc != FD_OK || n == 0) return rc;
+  int bits = isa_bits();
   if (bits == 512 && use_bf16_dot()) bits = 513;  // internal tag of the bf16-dot body
   const HostArgs a{q, q_stride_seq, q_stride_head, k_cache, v_cache, kv_stride_block,
                    kv_stride_head, kv_stride_token, num_blocks, block_table, bt_stride, bt_width,

@@ -442,37 +442,13 @@ class _HybridStaging:
 HYBRID_STAGING = _HybridStaging()
 
 
-class _HostShareRunner:
-    """One background thread per process that runs the host cores' share of
-    hybrid splits (the host-core kernel releases the GIL), so the share starts
-    as soon as q reaches the host rather than when the caller calls finish().
-    Recreated in a forked child, where the parent's thread does not exist."""
-
-    def __init__(self) -> None:
-        self._lock = threading.Lock()
-        self._pid = None
-        self._ex = None
-
-    def submit(self, fn):
-        import concurrent.futures
-
-        with self._lock:
-            if self._ex is None or self._pid != os.getpid():
-                self._ex = concurrent.futures.ThreadPoolExecutor(
-                    max_workers=1, thread_name_prefix="fd-host-share")
-                self._pid = os.getpid()
-            return self._ex.submit(fn)
-
-
-_HOST_SHARE = _HostShareRunner()
-
-
 class HybridSplit:
     """A hybrid split decode in flight (hybrid_split_begin): the GPU's share
-    is enqueued and the host cores' share runs in the background; finish()
-    waits for the latter and enqueues the merge."""
+    is enqueued and the host cores' share is queued on the library's runner
+    thread; finish() waits for the latter and enqueues the merge."""
 
-    def __init__(self, out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_fn=None, host_job=None,
+    def __init__(self, out, lse, o_gpu=None, l_gpu=None, o_cpu=None, l_cpu=None,
+                 host_call: HostDecodeCall | None = None, q_ready=None, gpu_done=None,
                  staging_idx=None, stream=None, owned=()):
         self.out, self.lse = out, lse
         # those of out / lse that begin() allocated (on its stream)
@@ -481,10 +457,10 @@ class HybridSplit:
         self._staging_idx, self._stream = staging_idx, stream
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
         self._o_cpu, self._l_cpu = o_cpu, l_cpu
-        # the host cores' share, and its future on the background thread; both
-        # give (host seconds, whether the GPU's launch was done at its end)
-        self._fn, self._job = host_fn, host_job
-        self.cpu_seconds = 0.0  # wall time of the host cores' share (0 before finish)
+        self._call = host_call
+        # events behind the copy of q to the host and behind the GPU's launch
+        self._q_ready, self._gpu_done = q_ready, gpu_done
+        self.cpu_seconds = 0.0  # time of the host cores' share (0 before finish)
         # whether the GPU's fused launch had completed when the host cores
         # finished (None before finish): the signal that balances the share
         self.gpu_finished_first: bool | None = None
@@ -494,7 +470,7 @@ class HybridSplit:
         # different streams if the caller switched streams in between
         HYBRID_STAGING.release(self._staging_idx,
                                (self._stream, torch.cuda.current_stream(self.out.device)))
-        self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._job = self._fn = None
+        self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._call = None
 
     def cancel(self) -> None:
         """Abandons a split that will not be finished (the caller's step
@@ -504,8 +480,7 @@ class HybridSplit:
         if self._o_gpu is None:
             return
         try:
-            if not self._job.cancel():  # already running: wait, whatever its outcome
-                self._job.exception()
+            self._call.wait()
         finally:
             self._drop()
 
@@ -516,10 +491,11 @@ class HybridSplit:
             return self.out, self.lse
         dev = self.out.device
         try:
-            # not picked up by the background thread yet: run it here instead
-            # (saves the thread hand-off when finish follows begin at once)
-            res = self._fn() if self._job.cancel() else self._job.result()
-            self.cpu_seconds, self.gpu_finished_first = res
+            self.cpu_seconds = self._call.wait()
+            # the GPU finished first if its launch is complete now and took no
+            # longer, from q's arrival on the host, than the host cores' share
+            self.gpu_finished_first = bool(self._gpu_done.query()) and (
+                self._q_ready.elapsed_time(self._gpu_done) <= self.cpu_seconds * 1e3)
             cur = torch.cuda.current_stream(dev)
             if self._stream is not None and cur != self._stream:
                 # the GPU partial (and out / lse when begin() allocated them)
@@ -531,8 +507,8 @@ class HybridSplit:
                               self._o_cpu.to(dev, non_blocking=True),
                               self._l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
         finally:
-            if self._job is not None and not self._job.done():
-                self._job.exception()  # finish interrupted: let the share stop first
+            if self._call is not None:
+                self._call.wait()  # finish interrupted: let the share stop first
             self._drop()
         return self.out, self.lse
 
@@ -556,13 +532,13 @@ def hybrid_split_begin(
     host_block_table_dev: torch.Tensor | None = None,
 ) -> HybridSplit:
     """First half of hybrid_split_decode: divides the host tier, starts the
-    copy of q to the host, enqueues the GPU's fused launch and then starts the
-    host cores' share on a background thread. Other GPU work can be enqueued
-    before HybridSplit.finish(), which waits for the host cores and enqueues
-    the merge. hbm_lens_dev /
-    host_block_table_dev: device copies of hbm_lens / host_block_table the
-    caller already holds (the GPU's share reads the host table unchanged,
-    only with shorter lengths), saving their uploads."""
+    copy of q to the host and queues the host cores' share behind it on the
+    library's runner thread (it starts as soon as q is on the host), then
+    enqueues the GPU's fused launch. Other GPU work can be enqueued before
+    HybridSplit.finish(), which waits for the host cores and enqueues the
+    merge. hbm_lens_dev / host_block_table_dev: device copies of hbm_lens /
+    host_block_table the caller already holds (the GPU's share reads the host
+    table unchanged, only with shorter lengths), saving their uploads."""
     _require(q.is_cuda and q.dim() == 3, "q must be [n, H, D] on the GPU")
     _require(host_block_table.device.type == "cpu" and host_lens.device.type == "cpu",
              "host_block_table and host_lens must be CPU tensors")
@@ -579,14 +555,21 @@ def hybrid_split_begin(
         owned.append(lse)
     share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
     if n == 0:
-        return HybridSplit(out, lse, None, None, None, None, None)
+        return HybridSplit(out, lse)
     stream = torch.cuda.current_stream(dev)
     idx = HYBRID_STAGING.acquire(dev)
+    call = None
     try:
         q_host = HYBRID_STAGING.view(idx, "q", q.shape, q.dtype)
         q_host.copy_(q, non_blocking=True)
-        q_ready = torch.cuda.Event()
+        q_ready = torch.cuda.Event(enable_timing=True)
         q_ready.record(stream)
+        o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
+        l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
+        # the host cores' blocks, from when q is on the host
+        call = host_decode_start(q_host, host_k_cache, host_v_cache, share.cpu_bt,
+                                 share.cpu_lens, softmax_scale, o_cpu, l_cpu,
+                                 num_threads=num_threads, ready=q_ready)
 
         def up(name, t):  # host index tensors: through pinned staging, asynchronous
             return HYBRID_STAGING.upload(idx, name, t, dev)
@@ -605,29 +588,17 @@ def hybrid_split_begin(
         split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table), hl,
                      host_k_cache, host_v_cache, hbt, up("gpu_lens", share.gpu_lens),
                      softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
-        gpu_done = torch.cuda.Event()
+        gpu_done = torch.cuda.Event(enable_timing=True)
         gpu_done.record(stream)
-        o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
-        l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
-
-        def host_share():  # the host cores' blocks, from when q is on the host
-            import time
-
-            q_ready.synchronize()
-            t0 = time.perf_counter()
-            host_decode_attn(q_host, host_k_cache, host_v_cache, share.cpu_bt, share.cpu_lens,
-                             softmax_scale, o_cpu, l_cpu, num_threads=num_threads)
-            return time.perf_counter() - t0, bool(gpu_done.query())
-
-        # submitted after the GPU's launch: the share's threads take every
-        # host core, and the launch path above would otherwise compete with
-        # them (measured slower when the GPU side bounds the step)
-        job = _HOST_SHARE.submit(host_share)
     except BaseException:
-        HYBRID_STAGING.release(idx, (stream,))
+        try:
+            if call is not None:
+                call.wait()  # the share reads the staging: let it stop first
+        finally:
+            HYBRID_STAGING.release(idx, (stream,))
         raise
-    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, host_share, job, staging_idx=idx,
-                       stream=stream, owned=tuple(owned))
+    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, call, q_ready, gpu_done,
+                       staging_idx=idx, stream=stream, owned=tuple(owned))
 
 
 def hybrid_split_decode(
@@ -746,13 +717,10 @@ def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse, row_ord
     )
 
 
-def host_decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse,
-                     num_threads: int = 0) -> None:
-    """Host-tier partial computed by the host cores (fd_host_decode_partial):
-    the signature and results of decode_attn above, i.e. of the reference's
-    decode_attn (fastdecode/csrc/cpu_attn.cpp:456-489), with every tensor in
-    host memory. Runs synchronously; num_threads 0 = one worker per CPU of
-    the affinity mask (or FASTDECODE_CPU_THREADS)."""
+def _host_decode_args(q, k_cache, v_cache, block_table, lens, scale, out, lse,
+                      num_threads: int):
+    """fd_host_decode_partial's arguments for host_decode_attn /
+    host_decode_start (None: no rows), after the checks both share."""
     for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache),
                     ("block_table", block_table), ("lens", lens), ("out", out), ("lse", lse)):
         _require(t.device.type == "cpu", f"{name} must be in host memory")
@@ -775,13 +743,10 @@ def host_decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse,
              and block_table.dim() == 2 and block_table.shape[0] == n and lens.shape == (n,),
              "block_table must be int32 [n, W] and lens int32 [n]")
     if n == 0:
-        return
+        return None
     _require(block_table.stride(1) == 1, "block_table rows must be contiguous")
-    lens = lens.contiguous()
-    lib = _lib.load_lib()
-    _lib.check(
-        lib.fd_host_decode_partial(
-            q.data_ptr(), q.stride(0), q.stride(1),
+    _require(lens.is_contiguous(), "lens must be contiguous")
+    return (q.data_ptr(), q.stride(0), q.stride(1),
             k_cache.data_ptr(), v_cache.data_ptr(),
             k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
             C,
@@ -791,9 +756,62 @@ def host_decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse,
             BS, float(scale), kv_dt,
             out.data_ptr(), out.stride(0), out.stride(1), _DT[out.dtype],
             lse.data_ptr(), lse.stride(0),
-            int(num_threads),
-        )
-    )
+            int(num_threads))
+
+
+def host_decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse,
+                     num_threads: int = 0) -> None:
+    """Host-tier partial computed by the host cores (fd_host_decode_partial):
+    the signature and results of decode_attn above, i.e. of the reference's
+    decode_attn (fastdecode/csrc/cpu_attn.cpp:456-489), with every tensor in
+    host memory. Runs synchronously; num_threads 0 = one worker per CPU of
+    the affinity mask (or FASTDECODE_CPU_THREADS)."""
+    args = _host_decode_args(q, k_cache, v_cache, block_table, lens.contiguous(), scale, out,
+                             lse, num_threads)
+    if args is not None:
+        _lib.check(_lib.load_lib().fd_host_decode_partial(*args))
+
+
+class HostDecodeCall:
+    """A host_decode_attn call queued on the library's runner thread
+    (fd_host_decode_partial_start). It holds the call's tensors until
+    wait(), which must be called once: it blocks until the call has run and
+    returns the seconds the call itself took."""
+
+    def __init__(self, call_id: int | None, keep: tuple) -> None:
+        self._id, self._keep = call_id, keep
+
+    def wait(self) -> float:
+        if self._id is None:  # no rows, or already waited for
+            self._keep = ()
+            return 0.0
+        secs = ctypes.c_double()
+        call_id, self._id = self._id, None
+        try:
+            _lib.check(_lib.load_lib().fd_host_decode_wait(call_id, ctypes.byref(secs)))
+        finally:
+            self._keep = ()
+        return secs.value
+
+
+def host_decode_start(q, k_cache, v_cache, block_table, lens, scale, out, lse,
+                      num_threads: int = 0, ready: torch.cuda.Event | None = None
+                      ) -> HostDecodeCall:
+    """host_decode_attn in the background: checks the arguments, queues the
+    call on the library's runner thread (fd_host_decode_partial_start) and
+    returns at once. The runner first waits for `ready` (e.g. an event
+    recorded behind the copy of q to the host). out / lse are written by the
+    time the returned call's wait() returns; until then no argument may be
+    changed or freed."""
+    lens = lens.contiguous()
+    args = _host_decode_args(q, k_cache, v_cache, block_table, lens, scale, out, lse,
+                             num_threads)
+    if args is None:
+        return HostDecodeCall(None, ())
+    ev = ready.cuda_event if ready is not None else None
+    call_id = ctypes.c_int64()
+    _lib.check(_lib.load_lib().fd_host_decode_partial_start(ev, *args, ctypes.byref(call_id)))
+    return HostDecodeCall(call_id.value, (q, k_cache, v_cache, block_table, lens, out, lse, ready))
 
 
 def paged_decode(
