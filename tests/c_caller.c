@@ -185,6 +185,17 @@ int main(void) {
       if (out[1][h][d] != 0.0f) return 10;
     if (!(isinf(lse[h][1]) && lse[h][1] < 0)) return 11;
   }
+  /* the same call queued on the library's runner thread: the same bits */
+  static float out2[N][H][D], lse2[H][N];
+  int64_t call = -1;
+  double secs = -1.0;
+  if (fd_host_decode_partial_start(NULL, q, H * D, D, kc, vc, KVH * BS * D, BS * D, D, C,
+                                   &bt[0][0], W, W, lens, N, H, KVH, D, BS, scale, FD_F32, out2,
+                                   H * D, D, FD_F32, &lse2[0][0], N, 2, &call) != FD_OK)
+    return 13;
+  if (fd_host_decode_wait(call, &secs) != FD_OK || secs < 0.0) return 14;
+  if (memcmp(out, out2, sizeof out2) != 0 || memcmp(lse, lse2, sizeof lse2) != 0) return 15;
+  if (fd_host_decode_wait(call, NULL) != FD_ERR_INVALID) return 16;
 #ifdef WITH_GPU
   if (gpu_case()) return 12;
 #endif
