@@ -281,3 +281,35 @@ def test_finish_on_another_stream_than_begin(gpu, given):
         rel = (lse.double().cpu()[:, nz] - ref_l[:, nz]).abs() / ref_l[:, nz].abs().clamp(min=1)
         assert float(rel.max()) <= 1e-4
         assert torch.all(out.cpu()[~nz] == 0)
+
+
+def test_host_call_waits_for_its_event(gpu):
+    """ops.host_decode_start with a ready event: q is copied to pinned memory
+    behind a slow GPU kernel on the stream and the event recorded after the
+    copy; the queued host call waits for it, so it reads the copied q (the
+    synchronous call on the same q gives the same bits). An event that was
+    never recorded is refused."""
+    from tests import cases
+    from vllm_fastdecoder_amd.pinned import pinned_empty
+
+    q, kc, vc, bt, lens = cases.rand_case(10, 8, 2, 128, 16, 90, torch.float16, 300, 21)
+    q_dev = q.to(gpu)
+    q_host = pinned_empty(tuple(q.shape), q.dtype)
+    q_host.zero_()
+    stream = torch.cuda.current_stream(gpu)
+    busy = torch.randn(4096, 4096, device=gpu)
+    for _ in range(20):  # keep the stream busy for a while before the copy
+        busy = (busy @ busy) * 1e-4
+    q_host.copy_(q_dev, non_blocking=True)
+    ready = torch.cuda.Event()
+    ready.record(stream)
+    out = torch.empty(10, 8, 128)
+    lse = torch.empty(8, 10)
+    call = ops.host_decode_start(q_host, kc, vc, bt, lens, 0.1, out, lse, ready=ready)
+    call.wait()
+    ref_o = torch.empty(10, 8, 128)
+    ref_l = torch.empty(8, 10)
+    ops.host_decode_attn(q, kc, vc, bt, lens, 0.1, ref_o, ref_l)
+    assert torch.equal(out, ref_o) and torch.equal(lse, ref_l)
+    with pytest.raises(RuntimeError, match="never recorded"):
+        ops.host_decode_start(q_host, kc, vc, bt, lens, 0.1, out, lse, ready=torch.cuda.Event())

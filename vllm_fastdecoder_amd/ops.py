@@ -808,7 +808,10 @@ def host_decode_start(q, k_cache, v_cache, block_table, lens, scale, out, lse,
                              num_threads)
     if args is None:
         return HostDecodeCall(None, ())
-    ev = ready.cuda_event if ready is not None else None
+    ev = None
+    if ready is not None:
+        ev = ready.cuda_event
+        _require(ev != 0, "host_decode_start: the ready event was never recorded")
     call_id = ctypes.c_int64()
     _lib.check(_lib.load_lib().fd_host_decode_partial_start(ev, *args, ctypes.byref(call_id)))
     return HostDecodeCall(call_id.value, (q, k_cache, v_cache, block_table, lens, out, lse, ready))
