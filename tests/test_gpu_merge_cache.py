@@ -58,6 +58,29 @@ def test_merge_matches_oracle(gpu, dtype, D):
         assert float(lerr.max()) <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_merge_reads_a_pinned_host_partial(gpu, dtype):
+    """o_b / lse_b in pinned host memory (the host cores' partial of the hybrid
+    split, read zero-copy over the link): the same bits as from HBM; pageable
+    host memory is refused."""
+    n, H, D = 9, 8, 128
+    o_a, lse_a, o_b, lse_b = _partials(n, H, D, dtype, D, gpu)
+    out_dev = torch.empty(n, H, D, dtype=dtype, device=gpu)
+    lse_dev = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    ops.merge_attn_states(out_dev, o_a, lse_a, o_b, lse_b, out_lse=lse_dev)
+    o_h = torch.empty(o_b.shape, dtype=o_b.dtype, pin_memory=True)
+    l_h = torch.empty(lse_b.shape, dtype=torch.float32, pin_memory=True)
+    o_h.copy_(o_b)
+    l_h.copy_(lse_b)
+    out = torch.full_like(out_dev, float("nan"))
+    olse = torch.empty_like(lse_dev)
+    ops.merge_attn_states(out, o_a, lse_a, o_h, l_h, out_lse=olse)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), out_dev.cpu()) and torch.equal(olse.cpu(), lse_dev.cpu())
+    with pytest.raises(RuntimeError, match="pinned memory"):
+        ops.merge_attn_states(out, o_a, lse_a, o_b.cpu(), lse_b.cpu())
+
+
 def test_merge_fa_empty_convention(gpu):
     """+inf LSE is empty: merge returns the other partial (test_cpu_kernel.py:141-147)."""
     o_a = torch.zeros(3, 2, 8, device=gpu)

@@ -503,9 +503,9 @@ class HybridSplit:
                 # them before this stream's merge and later work are done
                 for t in (self._o_gpu, self._l_gpu, *self._owned):
                     t.record_stream(cur)
-            merge_attn_states(self.out, self._o_gpu, self._l_gpu,
-                              self._o_cpu.to(dev, non_blocking=True),
-                              self._l_cpu.to(dev, non_blocking=True), out_lse=self.lse)
+            # the host partial is read by the merge straight from the pinned staging
+            merge_attn_states(self.out, self._o_gpu, self._l_gpu, self._o_cpu, self._l_cpu,
+                              out_lse=self.lse)
         finally:
             if self._call is not None:
                 self._call.wait()  # finish interrupted: let the share stop first
@@ -875,15 +875,19 @@ def paged_decode(
 
 def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
     """out = LSE-merge of two partials; vLLM merge_attn_states signature as
-    used at fastdecode/backend.py:53-55 (rule of cpu_ops.py:93-113)."""
+    used at fastdecode/backend.py:53-55 (rule of cpu_ops.py:93-113). o_b /
+    lse_b may also be views of pinned host memory (the host cores' partial):
+    the merge then reads them zero-copy over the link."""
     _require(out.dim() == 3 and o_a.shape == out.shape and o_b.shape == out.shape,
              "out, o_a, o_b must be [n, H, D] of one shape")
     n, H, D = out.shape
-    for t, name in ((out, "out"), (o_a, "o_a"), (o_b, "o_b")):
+    for t, name in ((out, "out"), (o_a, "o_a")):
         _require(t.is_cuda and t.stride(2) == 1, f"{name} must be a GPU tensor contiguous in D")
+    _require(o_b.stride(2) == 1, "o_b must be contiguous in D")
+    _require(lse_a.is_cuda, "lse_a must be on the GPU")
     for t, name in ((lse_a, "lse_a"), (lse_b, "lse_b")):
-        _require(t.is_cuda and t.dtype == torch.float32 and tuple(t.shape) == (H, n),
-                 f"{name} must be float32 [H, n] on the GPU")
+        _require(t.dtype == torch.float32 and tuple(t.shape) == (H, n),
+                 f"{name} must be float32 [H, n]")
         _require(n == 0 or t.stride(1) == 1, f"{name} rows must be contiguous")
     if out_lse is not None:
         _require(out_lse.dtype == torch.float32 and tuple(out_lse.shape) == (H, n) and
@@ -893,8 +897,8 @@ def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
             out.data_ptr(), out.stride(0), out.stride(1), _dtype_code(out, "out"),
             o_a.data_ptr(), o_a.stride(0), o_a.stride(1), _dtype_code(o_a, "o_a"),
             lse_a.data_ptr(), lse_a.stride(0),
-            o_b.data_ptr(), o_b.stride(0), o_b.stride(1), _dtype_code(o_b, "o_b"),
-            lse_b.data_ptr(), lse_b.stride(0),
+            device_ptr(o_b), o_b.stride(0), o_b.stride(1), _dtype_code(o_b, "o_b"),
+            device_ptr(lse_b), lse_b.stride(0),
             out_lse.data_ptr() if out_lse is not None else None,
             out_lse.stride(0) if out_lse is not None else 0,
             n, H, D,
