@@ -281,7 +281,7 @@ def host_tier_peaks(hk, hv, dev, threads, reps=5):
     over K and V, on the threads the host-core kernel uses), the GPU reading
     it over the link (fd_stream_copy from pinned memory into HBM), and both
     at once (the cores re-reading K in 128 MiB pieces while the GPU copies V
-    four times; each side's bytes over its own time)."""
+    four times; each side's bytes over its own time; the best of three)."""
     import torch
 
     from vllm_fastdecoder_amd import ops
@@ -301,30 +301,33 @@ def host_tier_peaks(hk, hv, dev, threads, reps=5):
     dst = torch.empty(vb, dtype=torch.uint8, device=dev)
     stream = torch.cuda.current_stream(dev)
     t_link = time_gpu(lambda: ops.stream_copy(dst, v8), reps, 1, stream)
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(4):
-        ops.stream_copy(dst, v8)
-    end.record(stream)
     piece = min(kb, 128 << 20) // 64 * 64
-    cpu_bytes, off = 0, 0
-    t0 = time.perf_counter()
-    while not end.query():
-        if off + piece > kb:
-            off = 0
-        ops.host_stream_read(k8[off: off + piece], threads)
-        off += piece
-        cpu_bytes += piece
-    t_cpu = time.perf_counter() - t0
-    end.synchronize()
-    t_gpu = start.elapsed_time(end) / 1e3
+    conc = []
+    for _ in range(3):  # the best of three (the two readers' overlap varies run to run)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(4):
+            ops.stream_copy(dst, v8)
+        end.record(stream)
+        cpu_bytes, off = 0, 0
+        t0 = time.perf_counter()
+        while not end.query():
+            if off + piece > kb:
+                off = 0
+            ops.host_stream_read(k8[off: off + piece], threads)
+            off += piece
+            cpu_bytes += piece
+        t_cpu = time.perf_counter() - t0
+        end.synchronize()
+        t_gpu = start.elapsed_time(end) / 1e3
+        c = cpu_bytes / t_cpu / 1e9 if t_cpu > 0 else 0.0
+        conc.append((c + 4 * vb / t_gpu / 1e9, c, 4 * vb / t_gpu / 1e9))
+    _, conc_cores, conc_link = max(conc)
     del dst
     cores_gbps = (kb + vb) / t_cores / 1e9
     link_gbps = vb / (t_link / 1e3) / 1e9
-    conc_cores = cpu_bytes / t_cpu / 1e9 if t_cpu > 0 else 0.0
-    conc_link = 4 * vb / t_gpu / 1e9
     return {
         "host_dram_read_GBps": round(cores_gbps, 1),
         "link_read_GBps": round(link_gbps, 2),
@@ -496,6 +499,7 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
     ref_ms, ref_cpu_ms, ref_kind = cpu_baseline_split_step(w, q, kc_g, vc_g, bt_g_d, len_g_d,
                                                            ord_g, hk, hv, bt_c, len_c, threads)
     host_gbps = kv_host / (t_auto / 1e3) / 1e9
+    peak = round(peaks["host_dram_read_GBps"] + peaks["link_read_GBps"], 1)
     del kv, hk, hv, q_host
     return {
         "host_fraction_blocks": 0.6,
@@ -521,12 +525,14 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
         "hybrid_auto_GBps": round((kv_hbm + kv_host) / (t_auto / 1e3) / 1e9, 1),
         "host_tier_bytes": kv_host,
         "roofline": {
-            "bound": "host DRAM (host cores and the link reading the pinned tier, measured "
-                     "together on this box)",
+            "bound": "host DRAM: the host cores streaming the pinned tier plus the link "
+                     "reading it, each rate measured alone on this box and summed (no "
+                     "division of the host tier between the two readers beats the sum)",
             "achieved": round(host_gbps, 1),
-            "peak": peaks["concurrent_GBps"],
+            "peak": peak,
             "unit": "GB/s",
-            "frac": round(host_gbps / peaks["concurrent_GBps"], 4),
+            "frac": round(host_gbps / peak, 4),
+            "frac_of_concurrent": round(host_gbps / peaks["concurrent_GBps"], 4),
             "frac_of_host_dram": round(host_gbps / peaks["host_dram_read_GBps"], 4),
             "kernel_ms": round(t_auto, 4),
             "note": "achieved = host-tier K+V bytes / hybrid step (share balanced online); "

@@ -419,14 +419,15 @@ class _HybridStaging:
         numel = 1
         for d in shape:
             numel *= int(d)
-        nbytes = max(numel * torch.empty(0, dtype=dtype).element_size(), 1)
+        used = numel * dtype.itemsize
+        nbytes = max(used, 1)
         with self._lock:
             buf = self._bufs.get((idx, name))
             if buf is None or buf.numel() < nbytes:
                 cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
                 buf = torch.empty(cap, dtype=torch.uint8, pin_memory=True)
                 self._bufs[(idx, name)] = buf
-        return buf[:numel * torch.empty(0, dtype=dtype).element_size()].view(dtype).view(shape)
+        return buf[:used].view(dtype).view(shape)
 
     def upload(self, idx: int, name: str, t: torch.Tensor, dev: torch.device) -> torch.Tensor:
         """A host tensor copied to the device through its pinned buffer (the
@@ -553,17 +554,20 @@ def hybrid_split_begin(
     if lse is None:
         lse = torch.empty(H, n, dtype=torch.float32, device=dev)
         owned.append(lse)
-    share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
     if n == 0:
+        _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
         return HybridSplit(out, lse)
     stream = torch.cuda.current_stream(dev)
     idx = HYBRID_STAGING.acquire(dev)
     call = None
     try:
+        # q on its way to the host first: the copy overlaps the share's host work
         q_host = HYBRID_STAGING.view(idx, "q", q.shape, q.dtype)
         q_host.copy_(q, non_blocking=True)
         q_ready = torch.cuda.Event(enable_timing=True)
         q_ready.record(stream)
+        share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2],
+                                   cpu_fraction)
         o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
         l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
         # the host cores' blocks, from when q is on the host

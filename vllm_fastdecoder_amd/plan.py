@@ -320,10 +320,12 @@ def share_host_blocks(host_bt: torch.Tensor, host_lens: torch.Tensor, block_size
     from . import _lib
 
     bt = host_bt.contiguous() if host_bt.stride(-1) != 1 else host_bt
-    lens = host_lens.to(torch.int32).contiguous()
+    lens = host_lens
+    if lens.dtype != torch.int32 or not lens.is_contiguous():
+        lens = lens.to(torch.int32).contiguous()
     n, W = bt.shape
-    gpu_lens = torch.empty(n, dtype=torch.int32)
-    cpu_lens = torch.empty(n, dtype=torch.int32)
+    both = torch.empty(2, n, dtype=torch.int32)  # gpu_lens, cpu_lens
+    gpu_lens, cpu_lens = both[0], both[1]
     cpu_bt = (torch.empty if W else torch.zeros)(n, max(W, 1), dtype=torch.int32)
     wc = ctypes.c_int32(0)
     _lib.check(_lib.load_lib().fd_share_host_blocks(
