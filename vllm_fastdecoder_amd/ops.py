@@ -467,8 +467,8 @@ class HybridSplit:
         self.gpu_finished_first: bool | None = None
 
     def _drop(self) -> None:
-        # begin's uploads and finish's copy of the host partial may sit on
-        # different streams if the caller switched streams in between
+        # begin's uploads and the merge's reads of the host partial may sit
+        # on different streams if the caller switched streams in between
         HYBRID_STAGING.release(self._staging_idx,
                                (self._stream, torch.cuda.current_stream(self.out.device)))
         self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._call = None
@@ -486,8 +486,8 @@ class HybridSplit:
             self._drop()
 
     def finish(self) -> tuple[torch.Tensor, torch.Tensor]:
-        """Waits for the host cores' share, uploads that partial and enqueues
-        the merge."""
+        """Waits for the host cores' share and enqueues the merge, which
+        reads that partial from the pinned staging."""
         if self._o_gpu is None:
             return self.out, self.lse
         dev = self.out.device
