@@ -67,7 +67,100 @@ def parse_args():
                          "host-core share (for a kernel trace of their GPU side)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run the 16-byte stream-copy kernel over MIB MiB (counter calibration)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only record per-workgroup time stamps of the workload's decode launches "
+                         "(fd_paged_decode_timeline; launches on the 16-bit VALU kernel), "
+                         "replayed from a HIP graph as the small-batch leg is")
     return ap.parse_args()
+
+
+def timeline_summary(w, steps, warmup, dev, copies):
+    """Per-workgroup time stamps of `steps` decode launches of workload w
+    (pool copies rotated, launches captured in one HIP graph after at least
+    100 ms of eager launches, as the small-batch leg runs), summarised as the
+    medians over launches of: the workgroups' start spread, the time to their
+    block ids, each task's end by its block count, and the rate at which a
+    task streams its blocks after its ids are in (bytes of its K and V over
+    the time from its ids to its last working wave's loop end)."""
+    import numpy as np
+    import torch
+
+    from vllm_fastdecoder_amd import ops
+
+    leg = DecodeLeg(w, "vllm", dev, copies=copies)
+    t0, k = time.perf_counter(), 0
+    while (time.perf_counter() - t0) < 0.1 or k < warmup:
+        leg.launch(k)
+        k += 1
+        if k % 8 == 0:
+            torch.cuda.synchronize()
+    tasks = w.n * w.KVH
+    tl = torch.zeros(steps, tasks, 8, dtype=torch.int64, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    ops.reserve_workspace(side, ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, leg.bt.shape[1]))
+
+    def launch(j):
+        kc, vc, _ = leg.pools[j % copies]
+        ops.paged_decode(leg.q, kc, vc, leg.bt_d, leg.lens_d, w.scale, out=leg.out, lse=leg.lse,
+                         row_order=leg.order_d, timeline=tl[j])
+
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for j in range(steps):
+            launch(j)
+    g.replay()
+    torch.cuda.synchronize()
+    tl.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    ops.release_workspace(side)
+    t = tl.cpu().numpy().astype(np.float64)
+    t = t[:, t[0, :, 0] > 0, :]  # workgroups that had a task
+    us = 0.01  # 100 MHz ticks
+    nblk = (t[0, :, 7].astype(np.int64) & 0xFFFF)
+    waves = (t[0, :, 7].astype(np.int64) >> 16) & 0xFF
+    bytes_per_block = 2 * w.BS * w.D * 2  # K + V of one (block, kv head)
+    per = []
+    for j in range(steps):
+        st = t[j, :, 0]
+        ref = st.min()
+        ids = t[j, :, 1] - st
+        loop_end = t[j, :, 2:6].max(axis=1)
+        end = t[j, :, 6] - ref
+        rate = nblk * bytes_per_block / np.maximum((loop_end - t[j, :, 1]) * us * 1e-6, 1e-9) / 1e9
+        per.append(dict(span=(t[j, :, 6].max() - ref) * us, start_spread=(st.max() - ref) * us,
+                        ids=np.median(ids) * us, ids_max=ids.max() * us,
+                        merge=np.median(t[j, :, 6] - loop_end) * us, end=end * us, rate=rate))
+    groups = {}
+    for lo, hi in ((1, 16), (17, 32), (33, 48), (49, 64), (65, 1 << 30)):
+        sel = (nblk >= lo) & (nblk <= hi)
+        if sel.any():
+            groups[f"{lo}-{hi if hi < 1 << 30 else 'up'} blocks"] = {
+                "tasks": int(sel.sum()),
+                "working_waves": sorted(set(waves[sel].tolist())),
+                "end_us_median": round(float(np.median([np.median(p["end"][sel]) for p in per])), 2),
+                "end_us_max": round(float(np.median([p["end"][sel].max() for p in per])), 2),
+                "stream_GBps_per_task": round(float(np.median([np.median(p["rate"][sel])
+                                                               for p in per])), 1),
+            }
+    med = lambda key: round(float(np.median([p[key] for p in per])), 2)  # noqa: E731
+    active = []  # tasks still running at each microsecond, median launch
+    span = med("span")
+    for x in range(int(span) + 1):
+        active.append(int(np.median([(p["end"] > x).sum() for p in per])))
+    return {
+        "workload": w.name, "launches": steps, "tasks_per_launch": int(t.shape[1]),
+        "span_us": span, "start_spread_us": med("start_spread"),
+        "ids_ready_us_median": med("ids"), "ids_ready_us_max": med("ids_max"),
+        "merge_and_store_us_median": med("merge"),
+        "by_task_blocks": groups,
+        "tasks_running_at_us": active,
+        "note": "workgroup stamps (s_memrealtime, 100 MHz) relative to the launch's first "
+                "workgroup start; medians over launches; stream rate = a task's K+V bytes over "
+                "the time from its block ids to its last working wave's loop end",
+    }
 
 
 def copy_calibration(mib: int, steps: int, warmup: int) -> int:
@@ -724,6 +817,10 @@ def main() -> int:
         return copy_calibration(args.copy_calibration, args.steps, args.warmup)
     w = cases.WORKLOADS[args.workload]
     lens, bt, pool = cases.draw_lens_and_tables(w)
+    if args.timeline:
+        copies = args.copies if args.copies is not None else (5 if w.name == "correctness" else 1)
+        print(json.dumps(timeline_summary(w, args.steps, args.warmup, dev, copies)))
+        return 0
     if args.hybrid_profile is not None:
         print(json.dumps(hybrid_profile(w, lens, bt, cases.queries(w, dev), args.hybrid_profile,
                                         args.steps, args.warmup, torch.cuda.current_stream(dev))))

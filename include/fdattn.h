@@ -167,6 +167,34 @@ int fd_paged_decode_partial_hint(
     void* workspace, size_t workspace_bytes,
     void* stream, int64_t total_tokens);
 
+/* Measurement helper: fd_paged_decode_partial (same arguments, same results)
+ * that also records when each workgroup of the decode launch reaches a few
+ * points, for launches that take the 16-bit VALU kernel (otherwise
+ * FD_ERR_UNSUPPORTED, nothing launched). timeline: a device buffer of
+ * timeline_workgroups * 8 uint64 (16-byte aligned, zeroed by the caller);
+ * a launch of more workgroups is FD_ERR_INVALID. Words of workgroup w, at
+ * timeline[8 w ...], in ticks of the GPU's 100 MHz real-time counter
+ * (s_memrealtime): 0 task start, 1 wave 0's block ids in registers, 2-5 each
+ * wave's end of its block loop, 6 the task's end (its result stored); word 7
+ * packs the task's block count (bits 0-15), its working waves (16-23) and
+ * its sequence (32-63). Workgroups with nothing to do leave their words
+ * unwritten. No counterpart in the reference; it splits a launch's time into
+ * start-up, streaming and drain. */
+int fd_paged_decode_timeline(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_stride, int32_t bt_width,
+    const int32_t* lens, const int32_t* row_order,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype,
+    float* lse, int64_t lse_stride_head,
+    void* workspace, size_t workspace_bytes,
+    void* stream, uint64_t* timeline, int64_t timeline_workgroups);
+
 /* Bytes of workspace fd_paged_decode_partial (and _hint, whatever its token
  * total) needs for these sizes (the block-range split partials), whatever
  * the kv dtype and wherever the cache lies: the largest need of the kernels

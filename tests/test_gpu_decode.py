@@ -778,3 +778,48 @@ def test_limits_of_the_tiled_kernels(gpu, H, KVH, D, BS, kernel, monkeypatch):
         assert_lse_close(lse, ref_lse, mask=nz)
         assert torch.all(out[~nz.to(gpu)] == 0)
         assert torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
+def test_timeline_launch_gives_the_same_bits_and_ordered_stamps(gpu):
+    """fd_paged_decode_timeline on the small-batch workload (one task per CU
+    on the VALU kernel): the same output and lse bits as the plain call, and
+    per workgroup start <= ids ready, start <= every wave's loop end <= task end
+    (a wave without blocks ends its loop at once),
+    with the task's block count and sequence in the info word. Launches that
+    take another kernel, or a buffer too short for the grid, are refused
+    before anything runs."""
+    w = cases.WORKLOADS["correctness"]
+    lens, bt, pool = cases.draw_lens_and_tables(w)
+    q = cases.queries(w, gpu)
+    kc, vc, _ = cases.kv_pool(w, pool, "vllm", gpu)
+    bt_d, lens_d = bt.to(gpu), lens.to(gpu)
+    ref_o, ref_l = ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale)
+    tl = torch.zeros(w.n * w.KVH, 8, dtype=torch.int64, device=gpu)
+    o, l = ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, timeline=tl)
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref_o) and torch.equal(l, ref_l)
+    t = tl.cpu()
+    assert bool((t[:, 0] > 0).all())
+    assert bool((t[:, 1] >= t[:, 0]).all())
+    for wv in range(4):
+        assert bool((t[:, 2 + wv] >= t[:, 0]).all())
+        assert bool((t[:, 6] >= t[:, 2 + wv]).all())
+    assert bool((t[:, 6] >= t[:, 1]).all())
+    info = t[:, 7]
+    nblk = info & 0xFFFF
+    seq = info >> 32
+    nb = (lens + w.BS - 1) // w.BS
+    assert torch.equal(nblk, nb[seq])
+    assert sorted(set(seq.tolist())) == list(range(w.n))
+    short = torch.zeros(w.n * w.KVH - 1, 8, dtype=torch.int64, device=gpu)
+    with pytest.raises(RuntimeError, match="room for"):
+        ops.paged_decode(q, kc, vc, bt_d, lens_d, w.scale, timeline=short)
+    # a grouped-query launch on the matrix-core kernel is refused
+    qg = torch.randn(16, 32, 128, device=gpu, dtype=torch.bfloat16)
+    kvg = torch.randn(64, 16, 8, 256, device=gpu, dtype=torch.bfloat16)
+    btg = torch.randint(0, 64, (16, 8), dtype=torch.int32, device=gpu)
+    lg = torch.full((16,), 100, dtype=torch.int32, device=gpu)
+    tlg = torch.zeros(1024, 8, dtype=torch.int64, device=gpu)
+    with pytest.raises(RuntimeError, match="VALU"):
+        ops.paged_decode(qg, kvg[..., :128], kvg[..., 128:], btg, lg, 0.1, timeline=tlg)
+    assert bool((tlg == 0).all())

@@ -181,7 +181,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 10; }
+int fd_abi_version(void) { return 11; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,
@@ -277,6 +277,31 @@ int fd_paged_decode_partial_hint(
                     num_kv_heads, head_size, block_size, scale, kv_dtype, out, out_stride_seq,
                     out_stride_head, out_dtype, lse, lse_stride_head, workspace,
                     workspace_bytes, stream, total_tokens);
+}
+
+int fd_paged_decode_timeline(
+    const void* q, int64_t q_stride_seq, int64_t q_stride_head, const void* k_cache,
+    const void* v_cache, int64_t kv_stride_block, int64_t kv_stride_head,
+    int64_t kv_stride_token, int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+    int32_t bt_width, const int32_t* lens, const int32_t* row_order, int32_t n,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_size, int32_t block_size, float scale,
+    int32_t kv_dtype, void* out, int64_t out_stride_seq, int64_t out_stride_head,
+    int32_t out_dtype, float* lse, int64_t lse_stride_head, void* workspace,
+    size_t workspace_bytes, void* stream, uint64_t* timeline, int64_t timeline_workgroups) {
+  if (timeline == nullptr || timeline_workgroups <= 0 || !aligned16(timeline))
+    return set_error(FD_ERR_INVALID,
+                     "decode_timeline: timeline must be a 16-byte aligned device buffer of at "
+                     "least one workgroup");
+  DecodeArgs a{};
+  a.tier[0] = KvTier{k_cache, v_cache, kv_stride_block, kv_stride_head, kv_stride_token,
+                     num_blocks, block_table, bt_stride, bt_width, lens};
+  a.ntiers = 1;
+  a.timeline = timeline;
+  a.timeline_tasks = timeline_workgroups;
+  return run_decode(a, "decode_timeline", q, q_stride_seq, q_stride_head, row_order, n,
+                    num_heads, num_kv_heads, head_size, block_size, scale, kv_dtype, out,
+                    out_stride_seq, out_stride_head, out_dtype, lse, lse_stride_head, workspace,
+                    workspace_bytes, stream);
 }
 
 int fd_split_decode(const void* q, int64_t q_stride_seq, int64_t q_stride_head,

@@ -606,6 +606,9 @@ size_t decode_workspace_bytes(const SplitPlan& sp, int32_t n, int32_t H, int32_t
 
 int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   if (a.n == 0) return FD_OK;
+  if (a.timeline != nullptr && (!sp.fast || sp.mm || sp.mfma || a.kv_dtype == FD_F32))
+    return set_error(FD_ERR_UNSUPPORTED,
+                     "decode_timeline: the launch takes another kernel than the 16-bit VALU one");
   const bool two = a.ntiers > 1;
   if (!sp.fast) {
     GenericParams gp{};
@@ -683,6 +686,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   tp.split_blocks = sp.split_blocks;
   tp.wave_blocks = sp.wave_blocks;
   tp.xcd_group = a.D % 64 != 0;
+  tp.timeline = a.timeline;
   const size_t parts = (size_t)a.n * a.H * sp.max_splits;
   if (sp.max_splits > 1) {
     char* ws = static_cast<char*>(a.workspace);
@@ -691,6 +695,9 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
   }
   const int64_t tasks = (int64_t)a.n * a.KVH * sp.passes * sp.max_splits;
   if (tasks > INT32_MAX) return set_error(FD_ERR_UNSUPPORTED, "decode: too many tasks");
+  if (a.timeline != nullptr && tasks > a.timeline_tasks)
+    return set_error(FD_ERR_INVALID, "decode_timeline: %lld workgroups, room for %lld",
+                     (long long)tasks, (long long)a.timeline_tasks);
   hipError_t e = dispatch_tiled(tp, (unsigned)tasks, sp, a.kv_dtype, a.D, two, s);
   if (e != hipSuccess) return hip_error(e, "decode kernel launch");
   if (sp.max_splits > 1) {

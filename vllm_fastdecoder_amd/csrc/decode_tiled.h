@@ -82,7 +82,15 @@ struct TiledParams {
   int32_t split_blocks;
   int32_t wave_blocks;  // blocks per working wave (0: every wave works; wave_blocks())
   bool xcd_group;   // adjacent kv heads of a row on one XCD (xcd_task)
+  uint64_t* timeline;  // measurement only: kTimelineSlots stamps per workgroup (NULL: none)
 };
+
+// Time stamps of one workgroup in a timeline launch (s_memrealtime, 100 MHz):
+// task start, wave 0's block ids in registers, each wave's end of its block
+// loop, the end of the task, and a word with the task's block count (bits
+// 0-15), working waves (16-23) and sequence (32-63).
+constexpr int kTimelineSlots = 8;
+enum TimelineSlot { kTlStart = 0, kTlIds = 1, kTlLoop0 = 2, kTlEnd = 6, kTlInfo = 7 };
 
 // Launchers of the kernel families (decode_valu.hip, decode_mfma.hip,
 // decode_mm.hip, decode_f32.hip).

@@ -22,7 +22,9 @@ namespace {
 // tier 0 keeps V right after K in each token row (vLLM's [B, BS, KVH, 2D]
 // cache; D = 128 or 256), and each load reads whole K + V runs of its tokens
 // (512 B at D = 128) instead of K and V rows in separate loads.
-template <typename T, int D, int G, bool TWO, bool ADJ, bool KEEP>
+// TL: a measurement build that records p.timeline (fd_paged_decode_timeline);
+// the production builds carry none of it.
+template <typename T, int D, int G, bool TWO, bool ADJ, bool KEEP, bool TL = false>
 __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(TiledParams p) {
   constexpr int LPT = D / 8;                // lanes per token row
   constexpr int TPW = kWave / LPT;          // token rows per load instruction
@@ -35,6 +37,17 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
   // The wave index is uniform across the wave; readfirstlane keeps it (and all
   // indexing derived from it) in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // measurement build only: lane 0 of the wave that reaches a point records
+  // the time
+  auto stamp = [&](int slot) {
+    if constexpr (TL) {
+      if (lane == 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        p.timeline[(int64_t)blockIdx.x * kTimelineSlots + slot] = __builtin_amdgcn_s_memrealtime();
+      }
+    }
+  };
+  if (wave == 0) stamp(kTlStart);
   Task t;
   if (!decode_task<G, TWO>(p, t)) return;
   if (t.nb == 0 || t.range_bad) {
@@ -93,6 +106,7 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
 
   const WaveBlocks wb = wave_blocks<TWO>(p, t, wave, lane);
   const int nw = wb.nw;
+  if (wave == 0) stamp(kTlIds);
   // the wave's block k read as K + V runs (tier 0 of an ADJ launch)
   auto adj_block = [&](int k) -> bool { return ADJ && !(TWO && k >= wb.k1); };
 
@@ -194,16 +208,29 @@ __global__ __launch_bounds__(kWave * kWavesPerTask) void decode_tiled_kernel(Til
     }
   }
 
+  stamp(kTlLoop0 + wave);
+
   // ---- merge the TPW lane-rows of each head into this wave's state, publish it
   publish_wave_state<D, G>(ws, wave, lane, m, l, acc, wb.bad);
   __syncthreads();
   if (wave != 0) return;
   finish_task<T, D, G>(p, t, ws, lane);
+  stamp(kTlEnd);
+  if constexpr (TL) {
+    if (lane == 0)
+      p.timeline[(int64_t)blockIdx.x * kTimelineSlots + kTlInfo] =
+          (uint64_t)(t.b_end - t.b_begin) | ((uint64_t)wb.stride << 16) |
+          ((uint64_t)(uint32_t)t.i << 32);
+  }
 }
 
 template <typename T, int D, int G, bool ADJ, bool KEEP>
 hipError_t launch_mode(const TiledParams& tp, unsigned tasks, const SplitPlan& sp, bool two,
                        hipStream_t s) {
+  if (tp.timeline != nullptr)  // a timeline launch (single tier: fd_paged_decode_timeline)
+    return two ? hipErrorInvalidValue
+               : launch_capped<&decode_tiled_kernel<T, D, G, false, ADJ, KEEP, true>>(tp, tasks,
+                                                                                      sp, s);
   return two ? launch_capped<&decode_tiled_kernel<T, D, G, true, ADJ, KEEP>>(tp, tasks, sp, s)
              : launch_capped<&decode_tiled_kernel<T, D, G, false, ADJ, KEEP>>(tp, tasks, sp, s);
 }

@@ -248,6 +248,11 @@ struct DecodeArgs {
   int64_t lse_sh;
   void* workspace;
   size_t workspace_bytes;
+  // measurement only (fd_paged_decode_timeline): per-workgroup time stamps
+  // of a VALU-kernel launch, kTimelineSlots words per workgroup; NULL in
+  // every other call
+  uint64_t* timeline;
+  int64_t timeline_tasks;
 };
 
 // Split plan of one decode call: blocks per split and the split count.

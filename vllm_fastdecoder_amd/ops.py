@@ -212,12 +212,16 @@ def paged_decode_partial(
     workspace: torch.Tensor | None = None,
     row_order: torch.Tensor | None = None,
     total_tokens: int | None = None,
+    timeline: torch.Tensor | None = None,
 ) -> None:
     """Layout-generic entry: kv_strides = (block, head, token) in elements.
     row_order: optional int32 [n] permutation scheduling the rows (e.g.
     longest_first(lens)); results do not depend on it. total_tokens: the
     rows' token total when the caller knows it on the host
-    (fd_paged_decode_partial_hint); it steers the task sizes only."""
+    (fd_paged_decode_partial_hint); it steers the task sizes only.
+    timeline: measurement only, a zeroed int64 [workgroups, 8] GPU tensor
+    that receives each workgroup's time stamps (fd_paged_decode_timeline;
+    launches on the 16-bit VALU kernel only)."""
     _require(q.is_cuda and out.is_cuda and lse.is_cuda, "q, out and lse must be on the GPU")
     _require(q.dim() == 3 and out.shape == q.shape, "q and out must be [n, H, D] of one shape")
     n, H, D = q.shape
@@ -269,7 +273,13 @@ def paged_decode_partial(
         ws_ptr, ws_len,
         _stream_for(q),
     )
-    if total_tokens is None:
+    if timeline is not None:
+        _require(total_tokens is None, "timeline: no token-total hint")
+        _require(timeline.is_cuda and timeline.dtype == torch.int64 and timeline.dim() == 2
+                 and timeline.shape[1] == 8 and timeline.is_contiguous(),
+                 "timeline must be a contiguous int64 [workgroups, 8] GPU tensor")
+        _lib.check(lib.fd_paged_decode_timeline(*args, timeline.data_ptr(), timeline.shape[0]))
+    elif total_tokens is None:
         _lib.check(lib.fd_paged_decode_partial(*args))
     else:
         _lib.check(lib.fd_paged_decode_partial_hint(*args, int(total_tokens)))
@@ -833,6 +843,7 @@ def paged_decode(
     row_order: torch.Tensor | None = None,
     max_seqlen_k: int | None = None,
     total_tokens: int | None = None,
+    timeline: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """HBM-tier partial in vLLM's paged layout: the decode call of
     flash_attn_varlen_func at fastdecode/backend.py:306-314 (one query token
@@ -854,6 +865,8 @@ def paged_decode(
     step's scheduler knows on the host): lets the launch plan tell rows of
     uneven length from equal ones, which want different task sizes. Results
     do not depend on it.
+
+    timeline: measurement only (see paged_decode_partial).
     """
     _require(key_cache.dim() == 4 and value_cache.shape == key_cache.shape,
              "key_cache/value_cache must be [B, BS, KVH, D]")
@@ -872,7 +885,7 @@ def paged_decode(
         q, key_cache, value_cache,
         (key_cache.stride(0), key_cache.stride(2), key_cache.stride(1)),
         B, BS, KVH, block_table, seqused_k, softmax_scale, out, lse, row_order=row_order,
-        total_tokens=total_tokens,
+        total_tokens=total_tokens, timeline=timeline,
     )
     return out, lse
 
