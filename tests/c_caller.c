@@ -6,7 +6,8 @@
  * with -DWITH_GPU (and the HIP runtime API, which is C), it also runs the
  * GPU entry point on device copies of a larger fp32 case (16-token blocks:
  * the tiled fp32 kernel), with and without the rows' token total, and checks
- * it the same way.
+ * it the same way, and a whole hybrid split step (host cores and GPU on the
+ * host tier, merged on the GPU).
  * Exit status 0 = every check passed; otherwise the number of the check. */
 #include <math.h>
 #include <stdint.h>
@@ -139,6 +140,134 @@ static int gpu_case(void) {
   if (dws) hipFree(dws);
   return 0;
 }
+
+/* The hybrid split step from C: an HBM tier in device memory and a host tier
+ * in pinned memory (fd_host_alloc); the host cores' share queued behind the
+ * copy of q to the host (fd_host_decode_partial_start), the GPU's fused launch
+ * over the HBM tier and the leading host blocks (fd_split_decode), then
+ * fd_host_decode_wait and the merge reading the host partial in place. Rows
+ * of 50 (32 in HBM + 18 on the host), 0 and 56 (16 + 40) tokens, half of each
+ * row's host blocks to the host cores; checked against double-precision
+ * attention over each row's blocks of both tiers. */
+enum { HG = 6, HC = 8 }; /* HBM blocks, host blocks */
+static float hk_all[HG + HC][GKVH][GBS][GD], hv_all[HG + HC][GKVH][GBS][GD];
+static float hq[GN][GH][GD], hout[GN][GH][GD], hlse[GH][GN];
+
+static int hybrid_case(void) {
+  int32_t hbm_bt[GN][GW] = {{4, 1, 0, 0}, {0, 0, 0, 0}, {5, 0, 0, 0}};
+  int32_t host_bt[GN][GW] = {{6, 2, 0, 0}, {0, 0, 0, 0}, {0, 7, 3, 0}};
+  int32_t hbm_lens[GN] = {32, 0, 16}, host_lens[GN] = {18, 0, 40};
+  unsigned s = 4242;
+  for (int i = 0; i < GN; ++i)
+    for (int h = 0; h < GH; ++h)
+      for (int d = 0; d < GD; ++d) hq[i][h][d] = val(s++);
+  for (int b = 0; b < HG + HC; ++b)
+    for (int kh = 0; kh < GKVH; ++kh)
+      for (int t = 0; t < GBS; ++t)
+        for (int d = 0; d < GD; ++d) {
+          hk_all[b][kh][t][d] = val(s++);
+          hv_all[b][kh][t][d] = val(s++);
+        }
+  const size_t blk = sizeof hk_all[0];
+  const int64_t sb = GKVH * GBS * GD, sh = GBS * GD, st = GD;
+  /* pinned host tier, q staging and host partial */
+  void *hk, *hv, *q_host, *o_host, *l_host, *hk_d, *hv_d, *o_host_d, *l_host_d;
+  if (fd_host_alloc(HC * blk, &hk) || fd_host_alloc(HC * blk, &hv) ||
+      fd_host_alloc(sizeof hq, &q_host) || fd_host_alloc(sizeof hout, &o_host) ||
+      fd_host_alloc(sizeof hlse, &l_host))
+    return 20;
+  if (fd_host_device_pointer(hk, &hk_d) || fd_host_device_pointer(hv, &hv_d) ||
+      fd_host_device_pointer(o_host, &o_host_d) || fd_host_device_pointer(l_host, &l_host_d))
+    return 21;
+  memcpy(hk, hk_all[HG], HC * blk);
+  memcpy(hv, hv_all[HG], HC * blk);
+  /* device side: q, the HBM tier, the tables, the GPU partial and the output */
+  void *dq, *dk, *dv, *dhbt, *dhl, *dhost_bt, *dgl, *dog, *dlg, *dout, *dlse, *dws = NULL;
+  size_t ws = 0;
+  if (fd_paged_decode_workspace_size(GN, GH, GKVH, GD, GBS, 2 * GW, &ws) != FD_OK) return 22;
+  if (hipMalloc(&dq, sizeof hq) || hipMalloc(&dk, HG * blk) || hipMalloc(&dv, HG * blk) ||
+      hipMalloc(&dhbt, sizeof hbm_bt) || hipMalloc(&dhl, sizeof hbm_lens) ||
+      hipMalloc(&dhost_bt, sizeof host_bt) || hipMalloc(&dgl, sizeof host_lens) ||
+      hipMalloc(&dog, sizeof hout) || hipMalloc(&dlg, sizeof hlse) ||
+      hipMalloc(&dout, sizeof hout) || hipMalloc(&dlse, sizeof hlse) ||
+      (ws > 0 && hipMalloc(&dws, ws)))
+    return 23;
+  if (hipMemcpy(dq, hq, sizeof hq, hipMemcpyHostToDevice) ||
+      hipMemcpy(dk, hk_all, HG * blk, hipMemcpyHostToDevice) ||
+      hipMemcpy(dv, hv_all, HG * blk, hipMemcpyHostToDevice) ||
+      hipMemcpy(dhbt, hbm_bt, sizeof hbm_bt, hipMemcpyHostToDevice) ||
+      hipMemcpy(dhl, hbm_lens, sizeof hbm_lens, hipMemcpyHostToDevice) ||
+      hipMemcpy(dhost_bt, host_bt, sizeof host_bt, hipMemcpyHostToDevice))
+    return 24;
+  /* 1. divide each row's host blocks: half to the host cores */
+  int32_t gpu_lens[GN], cpu_lens[GN], cpu_bt[GN][GW], wc = 0;
+  if (fd_share_host_blocks(&host_bt[0][0], GW, GW, host_lens, GN, GBS, 0.5, gpu_lens,
+                           &cpu_bt[0][0], GW, cpu_lens, &wc) != FD_OK)
+    return 25;
+  if (hipMemcpy(dgl, gpu_lens, sizeof gpu_lens, hipMemcpyHostToDevice)) return 24;
+  /* 2. q to the host and the host cores' share queued behind it */
+  hipEvent_t q_ready;
+  if (hipEventCreate(&q_ready) || hipMemcpyAsync(q_host, dq, sizeof hq, hipMemcpyDeviceToHost, NULL) ||
+      hipEventRecord(q_ready, NULL))
+    return 26;
+  const float scale = 0.125f;
+  int64_t call = -1;
+  if (fd_host_decode_partial_start(q_ready, q_host, GH * GD, GD, hk, hv, sb, sh, st, HC,
+                                   &cpu_bt[0][0], GW, GW, cpu_lens, GN, GH, GKVH, GD, GBS, scale,
+                                   FD_F32, o_host, GH * GD, GD, FD_F32, (float*)l_host, GN, 2,
+                                   &call) != FD_OK) {
+    fprintf(stderr, "%s\n", fd_last_error());
+    return 27;
+  }
+  /* 3. the GPU's share: the HBM tier and the leading host blocks, zero-copy */
+  fd_kv_tier hbm = {dk, dv, sb, sh, st, HG, (const int32_t*)dhbt, GW, GW, (const int32_t*)dhl};
+  fd_kv_tier host = {hk_d, hv_d, sb, sh, st, HC, (const int32_t*)dhost_bt, GW, GW,
+                     (const int32_t*)dgl};
+  if (fd_split_decode(dq, GH * GD, GD, &hbm, &host, NULL, GN, GH, GKVH, GD, GBS, scale, FD_F32,
+                      dog, GH * GD, GD, FD_F32, (float*)dlg, GN, dws, ws, NULL) != FD_OK) {
+    fprintf(stderr, "%s\n", fd_last_error());
+    fd_host_decode_wait(call, NULL);
+    return 28;
+  }
+  /* 4. wait for the host cores, then merge reading their partial in place */
+  double secs = -1.0;
+  if (fd_host_decode_wait(call, &secs) != FD_OK || secs < 0.0) return 29;
+  if (fd_merge_attn_states(dout, GH * GD, GD, FD_F32, dog, GH * GD, GD, FD_F32, (const float*)dlg,
+                           GN, o_host_d, GH * GD, GD, FD_F32, (const float*)l_host_d, GN,
+                           (float*)dlse, GN, GN, GH, GD, NULL) != FD_OK) {
+    fprintf(stderr, "%s\n", fd_last_error());
+    return 30;
+  }
+  if (hipDeviceSynchronize() || hipMemcpy(hout, dout, sizeof hout, hipMemcpyDeviceToHost) ||
+      hipMemcpy(hlse, dlse, sizeof hlse, hipMemcpyDeviceToHost))
+    return 31;
+  /* each row's blocks of both tiers as one table over hk_all / hv_all */
+  for (int i = 0; i < GN; ++i) {
+    int32_t both[2 * GW];
+    const int nh = (hbm_lens[i] + GBS - 1) / GBS, nc = (host_lens[i] + GBS - 1) / GBS;
+    for (int b = 0; b < nh; ++b) both[b] = hbm_bt[i][b];
+    for (int b = 0; b < nc; ++b) both[nh + b] = HG + host_bt[i][b];
+    const int32_t len = hbm_lens[i] + host_lens[i];
+    for (int h = 0; h < GH; ++h) {
+      if (len == 0) {
+        for (int d = 0; d < GD; ++d)
+          if (hout[i][h][d] != 0.0f) return 32;
+        if (!(isinf(hlse[h][i]) && hlse[h][i] < 0)) return 33;
+      } else if (check_row(hq[i][h], &hk_all[0][0][0][0], &hv_all[0][0][0][0], both, len,
+                           h / (GH / GKVH), GKVH, GBS, GD, scale, hout[i][h], hlse[h][i])) {
+        return 34;
+      }
+    }
+  }
+  hipEventDestroy(q_ready);
+  hipFree(dq); hipFree(dk); hipFree(dv); hipFree(dhbt); hipFree(dhl); hipFree(dhost_bt);
+  hipFree(dgl); hipFree(dog); hipFree(dlg); hipFree(dout); hipFree(dlse);
+  if (dws) hipFree(dws);
+  if (fd_host_free(hk) || fd_host_free(hv) || fd_host_free(q_host) || fd_host_free(o_host) ||
+      fd_host_free(l_host))
+    return 35;
+  return 0;
+}
 #endif
 
 int main(void) {
@@ -198,6 +327,8 @@ int main(void) {
   if (fd_host_decode_wait(call, NULL) != FD_ERR_INVALID) return 16;
 #ifdef WITH_GPU
   if (gpu_case()) return 12;
+  const int hyb = hybrid_case();
+  if (hyb) return hyb;
 #endif
   printf("c caller ok (workspace for the query: %zu bytes)\n", ws);
   return 0;
