@@ -50,7 +50,10 @@ def _build(tmp_path, gpu: bool):
 def test_plain_c_caller_on_the_gpu(gpu, tmp_path):
     """The same C caller with its GPU section: device copies through the HIP
     runtime API (C), fd_paged_decode_partial on fp32 KV in 16-token blocks
-    (the tiled fp32 kernel), checked against double-precision attention."""
+    (the tiled fp32 kernel), and a whole hybrid split step (the host share
+    queued behind q's copy, the fused launch over both tiers, the merge of
+    the pinned host partial), each checked against double-precision
+    attention."""
     exe = _build(tmp_path, gpu=True)
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0, f"check {run.returncode} failed: {run.stdout}{run.stderr}"
