@@ -94,7 +94,8 @@ def timeline_summary(w, steps, warmup, dev, copies):
         k += 1
         if k % 8 == 0:
             torch.cuda.synchronize()
-    tasks = w.n * w.KVH
+    plan = ops.decode_plan_info(w.n, w.H, w.KVH, w.D, w.BS, leg.bt.shape[1], w.dtype)
+    tasks = w.n * w.KVH * plan["passes"] * plan["max_splits"]
     tl = torch.zeros(steps, tasks, 8, dtype=torch.int64, device=dev)
     side = torch.cuda.Stream(device=dev)
     ops.reserve_workspace(side, ops.workspace_bytes(w.n, w.H, w.KVH, w.D, w.BS, leg.bt.shape[1]))
@@ -554,13 +555,18 @@ def split_run(w, lens, bt, q, steps, warmup, stream):
                                                w.scale, frac, out=h_out, lse=h_lse)
 
     host_steps = max(2, min(steps, 5))
-    host_cores()
-    t0 = time.perf_counter()
-    for _ in range(host_steps):
+    # the host cores alone: 3 warm-ups, then the median of 10 calls (the host's
+    # DRAM reads run slower for the first calls after idling)
+    for _ in range(3):
         host_cores()
-    t_cores = (time.perf_counter() - t0) / host_steps * 1e3
+    ts = []
+    for _ in range(10):
+        t0 = time.perf_counter()
+        host_cores()
+        ts.append(time.perf_counter() - t0)
+    t_cores = sorted(ts)[len(ts) // 2] * 1e3
     fracs = (0.5, 0.6, 0.7, 0.8, 0.9)
-    t_hybrid = {f: time_gpu(hybrid(f), host_steps, 1, stream) for f in fracs}
+    t_hybrid = {f: time_gpu(hybrid(f), 10, 3, stream) for f in fracs}
     f_best = min(t_hybrid, key=t_hybrid.get)
     # the share balanced online (SplitDecodeImpl(cpu_fraction="auto"))
     from vllm_fastdecoder_amd.plan import ShareTuner
