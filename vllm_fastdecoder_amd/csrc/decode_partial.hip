@@ -666,7 +666,10 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     tt.bt_width = kt.bt_width;
     tt.lens = kt.lens;
   }
-  tp.order = a.order;
+  // in a launch of at most one task per CU (working waves by row length) every
+  // task starts at once, so the dispatch order changes nothing; without it a
+  // task's first dependent load (its row's place in the order) goes away
+  tp.order = sp.wave_blocks > 0 ? nullptr : a.order;
   tp.n = a.n;
   tp.H = a.H;
   tp.KVH = a.KVH;
