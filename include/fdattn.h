@@ -545,6 +545,37 @@ int fd_share_host_blocks(const int32_t* host_bt, int64_t bt_stride, int32_t bt_w
                          double cpu_fraction, int32_t* gpu_lens, int32_t* cpu_bt,
                          int64_t cpu_bt_stride, int32_t* cpu_lens, int32_t* cpu_width);
 
+/* The host cores' share of a hybrid split step, started in one call (no
+ * counterpart in the reference, whose host cores take the whole host tier
+ * synchronously after staging q, fastdecode/backend.py:343-351). In order:
+ *   1. enqueues on `stream` the copy of q (the GPU's [n, H, D], contiguous,
+ *      kv_dtype) to q_host (pinned host memory of the same layout) and
+ *      records ready_event (a hipEvent_t) behind it;
+ *   2. divides each row's host-tier blocks as fd_share_host_blocks does
+ *      (writes gpu_lens, cpu_bt, cpu_lens; cpu_bt's rows hold
+ *      max(bt_width, 1) ids, cpu_bt_stride apart);
+ *   3. queues, as fd_host_decode_partial_start does, fd_host_decode_partial
+ *      over the host cores' blocks (q_host, cpu_bt, cpu_lens) into out (fp32
+ *      [n, H, D], contiguous) and lse (fp32 [H, n], contiguous) behind
+ *      ready_event, and returns at once with *call for fd_host_decode_wait.
+ * The arguments are checked first (an invalid call enqueues and queues
+ * nothing); a table row needing more than bt_width blocks fails in step 2,
+ * after the copy was enqueued, and queues no call. n = 0: nothing is done
+ * and *call = 0 (nothing to wait for). Replaces the copy, the share and the
+ * start that a caller would otherwise make one by one, which cost the step
+ * ~0.1 ms of host time between the host cores' shares. */
+int fd_hybrid_share_start(
+    void* stream, void* ready_event, const void* q, void* q_host,
+    const int32_t* host_bt, int64_t bt_stride, int32_t bt_width,
+    const int32_t* host_lens, double cpu_fraction,
+    int32_t* gpu_lens, int32_t* cpu_bt, int64_t cpu_bt_stride, int32_t* cpu_lens,
+    const void* k_cache, const void* v_cache,
+    int64_t kv_stride_block, int64_t kv_stride_head, int64_t kv_stride_token,
+    int64_t num_blocks,
+    int32_t n, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+    int32_t block_size, float scale, int32_t kv_dtype,
+    float* out, float* lse, int32_t num_threads, int64_t* call);
+
 /* Host-tier slot write on the host cores: the reference's store_kv
  * (cpu_attn.cpp:491-517, body :413-431) with host pointers.
  *   cache[slot / BS][kv head][slot % BS][:] = k[j][kv head][:]  (and V)

@@ -153,7 +153,8 @@ enum { HG = 6, HC = 8 }; /* HBM blocks, host blocks */
 static float hk_all[HG + HC][GKVH][GBS][GD], hv_all[HG + HC][GKVH][GBS][GD];
 static float hq[GN][GH][GD], hout[GN][GH][GD], hlse[GH][GN];
 
-static int hybrid_case(void) {
+/* one_call: steps 1-2 below as the single fd_hybrid_share_start call */
+static int hybrid_case(int one_call) {
   int32_t hbm_bt[GN][GW] = {{4, 1, 0, 0}, {0, 0, 0, 0}, {5, 0, 0, 0}};
   int32_t host_bt[GN][GW] = {{6, 2, 0, 0}, {0, 0, 0, 0}, {0, 7, 3, 0}};
   int32_t hbm_lens[GN] = {32, 0, 16}, host_lens[GN] = {18, 0, 40};
@@ -201,24 +202,36 @@ static int hybrid_case(void) {
     return 24;
   /* 1. divide each row's host blocks: half to the host cores */
   int32_t gpu_lens[GN], cpu_lens[GN], cpu_bt[GN][GW], wc = 0;
-  if (fd_share_host_blocks(&host_bt[0][0], GW, GW, host_lens, GN, GBS, 0.5, gpu_lens,
-                           &cpu_bt[0][0], GW, cpu_lens, &wc) != FD_OK)
-    return 25;
-  if (hipMemcpy(dgl, gpu_lens, sizeof gpu_lens, hipMemcpyHostToDevice)) return 24;
-  /* 2. q to the host and the host cores' share queued behind it */
   hipEvent_t q_ready;
-  if (hipEventCreate(&q_ready) || hipMemcpyAsync(q_host, dq, sizeof hq, hipMemcpyDeviceToHost, NULL) ||
-      hipEventRecord(q_ready, NULL))
-    return 26;
+  if (hipEventCreate(&q_ready)) return 26;
   const float scale = 0.125f;
   int64_t call = -1;
-  if (fd_host_decode_partial_start(q_ready, q_host, GH * GD, GD, hk, hv, sb, sh, st, HC,
-                                   &cpu_bt[0][0], GW, GW, cpu_lens, GN, GH, GKVH, GD, GBS, scale,
-                                   FD_F32, o_host, GH * GD, GD, FD_F32, (float*)l_host, GN, 2,
-                                   &call) != FD_OK) {
-    fprintf(stderr, "%s\n", fd_last_error());
-    return 27;
+  if (one_call) {
+    /* 1-2 in one call: q to the host, the division, the share queued */
+    if (fd_hybrid_share_start(NULL, q_ready, dq, q_host, &host_bt[0][0], GW, GW, host_lens, 0.5,
+                              gpu_lens, &cpu_bt[0][0], GW, cpu_lens, hk, hv, sb, sh, st, HC, GN,
+                              GH, GKVH, GD, GBS, scale, FD_F32, (float*)o_host, (float*)l_host, 2,
+                              &call) != FD_OK) {
+      fprintf(stderr, "%s\n", fd_last_error());
+      return 27;
+    }
+  } else {
+    if (fd_share_host_blocks(&host_bt[0][0], GW, GW, host_lens, GN, GBS, 0.5, gpu_lens,
+                             &cpu_bt[0][0], GW, cpu_lens, &wc) != FD_OK)
+      return 25;
+    /* 2. q to the host and the host cores' share queued behind it */
+    if (hipMemcpyAsync(q_host, dq, sizeof hq, hipMemcpyDeviceToHost, NULL) ||
+        hipEventRecord(q_ready, NULL))
+      return 26;
+    if (fd_host_decode_partial_start(q_ready, q_host, GH * GD, GD, hk, hv, sb, sh, st, HC,
+                                     &cpu_bt[0][0], GW, GW, cpu_lens, GN, GH, GKVH, GD, GBS,
+                                     scale, FD_F32, o_host, GH * GD, GD, FD_F32, (float*)l_host,
+                                     GN, 2, &call) != FD_OK) {
+      fprintf(stderr, "%s\n", fd_last_error());
+      return 27;
+    }
   }
+  if (hipMemcpy(dgl, gpu_lens, sizeof gpu_lens, hipMemcpyHostToDevice)) return 24;
   /* 3. the GPU's share: the HBM tier and the leading host blocks, zero-copy */
   fd_kv_tier hbm = {dk, dv, sb, sh, st, HG, (const int32_t*)dhbt, GW, GW, (const int32_t*)dhl};
   fd_kv_tier host = {hk_d, hv_d, sb, sh, st, HC, (const int32_t*)dhost_bt, GW, GW,
@@ -327,8 +340,15 @@ int main(void) {
   if (fd_host_decode_wait(call, NULL) != FD_ERR_INVALID) return 16;
 #ifdef WITH_GPU
   if (gpu_case()) return 12;
-  const int hyb = hybrid_case();
+  const int hyb = hybrid_case(0);
   if (hyb) return hyb;
+  static float first_out[GN][GH][GD], first_lse[GH][GN];
+  memcpy(first_out, hout, sizeof hout);
+  memcpy(first_lse, hlse, sizeof hlse);
+  const int hyb1 = hybrid_case(1);
+  if (hyb1) return hyb1;
+  /* the one-call start divides and computes exactly as the separate calls */
+  if (memcmp(first_out, hout, sizeof hout) || memcmp(first_lse, hlse, sizeof hlse)) return 36;
 #endif
   printf("c caller ok (workspace for the query: %zu bytes)\n", ws);
   return 0;

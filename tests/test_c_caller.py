@@ -53,7 +53,8 @@ def test_plain_c_caller_on_the_gpu(gpu, tmp_path):
     (the tiled fp32 kernel), and a whole hybrid split step (the host share
     queued behind q's copy, the fused launch over both tiers, the merge of
     the pinned host partial), each checked against double-precision
-    attention."""
+    attention; the hybrid step twice, by separate calls and with
+    fd_hybrid_share_start, bit-identical."""
     exe = _build(tmp_path, gpu=True)
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
     assert run.returncode == 0, f"check {run.returncode} failed: {run.stdout}{run.stderr}"

@@ -340,6 +340,47 @@ def test_host_decode_start_checks_before_queueing():
     assert torch.isfinite(o2[0]).all()
 
 
+def test_hybrid_share_start_checks_before_any_work():
+    """fd_hybrid_share_start refuses bad arguments before it enqueues the copy
+    of q or queues a call (nothing written, *call 0), and n = 0 does nothing.
+    None of these paths reaches the GPU."""
+    lib = _lib.load_lib()
+    q, kc, vc, bt, lens = cases.rand_case(2, 4, 2, 64, 16, 8, torch.float16, 30, 0)
+    W = bt.shape[1]
+    q_host = torch.empty_like(q)
+    gl = torch.full((2,), -7, dtype=torch.int32)
+    cl = torch.full((2,), -7, dtype=torch.int32)
+    cbt = torch.full((2, W), -7, dtype=torch.int32)
+    out = torch.full((2, 4, 64), -7.0)
+    lse = torch.full((4, 2), -7.0)
+    fake = ctypes.c_void_p(0x1000)  # a stream / event / GPU q no path below may touch
+
+    def start(n=2, H=4, frac=0.5, cbt_stride=W, event=fake, threads=0, call=True):
+        c = ctypes.c_int64(-1)
+        st = lib.fd_hybrid_share_start(
+            fake, event, fake, q_host.data_ptr(), bt.data_ptr(), bt.stride(0), W,
+            lens.data_ptr(), frac, gl.data_ptr(), cbt.data_ptr(), cbt_stride, cl.data_ptr(),
+            kc.data_ptr(), vc.data_ptr(), kc.stride(0), kc.stride(1), kc.stride(2), 8,
+            n, H, 2, 64, 16, 0.1, _lib.FD_F16, out.data_ptr(), lse.data_ptr(), threads,
+            ctypes.byref(c) if call else None)
+        return st, c.value
+
+    assert start(call=False)[0] == _lib.FD_ERR_INVALID
+    assert b"call is NULL" in lib.fd_last_error()
+    for kw, msg in ((dict(H=3), b"bad sizes"), (dict(frac=1.5), b"cpu_fraction"),
+                    (dict(frac=float("nan")), b"cpu_fraction"),
+                    (dict(cbt_stride=W - 1), b"bt_stride < bt_width"),
+                    (dict(event=None), b"NULL pointer"),
+                    (dict(threads=1025), b"bad sizes")):
+        st, c = start(**kw)
+        assert st == _lib.FD_ERR_INVALID and msg in lib.fd_last_error(), kw
+        assert c == 0
+    assert start(n=0) == (_lib.FD_OK, 0)
+    for t in (gl, cl, cbt):
+        assert (t == -7).all()
+    assert (out == -7).all() and (lse == -7).all()
+
+
 def _child_start(conn, args):
     q, kc, vc, bt, lens = args
     out = torch.empty(q.shape, dtype=torch.float32)

@@ -94,6 +94,26 @@ def test_task_split_follows_the_override(monkeypatch):
     assert p["split_blocks"] == 64 and p["max_splits"] == 4 and p["capped"]
 
 
+def test_tuning_variables_match_whole_names(monkeypatch):
+    """The planner reads its tuning variables in one pass over the
+    environment: each counts under its exact name only, and a longer name
+    sharing its prefix, or the name without FD_, changes nothing."""
+    base = plan(4, 32, 8, 128, 100)
+    for name in ("FD_SPLIT_BLOCKSX", "FD_SPLIT_BLOCK", "SPLIT_BLOCKS", "XFD_SPLIT_BLOCKS"):
+        monkeypatch.setenv(name, "16")
+    monkeypatch.setenv("FD_DECODE_KERNEL_", "mfma")
+    monkeypatch.setenv("FD_WG_CAPS", "1")
+    assert plan(4, 32, 8, 128, 100) == base
+    monkeypatch.setenv("FD_WG_CAP", "1")
+    monkeypatch.setenv("FD_WAVE_BLOCKS", "5")
+    p = plan(4, 32, 8, 128, 100)
+    assert p["wg_cap"] == 1 and p["capped"] and p["wave_blocks"] == 5
+    monkeypatch.setenv("FD_WG_CAP", "")      # empty: no cap from the variable
+    monkeypatch.setenv("FD_WAVE_BLOCKS", "-3")  # negative: every wave works
+    p = plan(4, 32, 8, 128, 100)
+    assert p["wg_cap"] == base["wg_cap"] and p["wave_blocks"] == 0
+
+
 def test_task_size_follows_the_block_bytes():
     """The launch-time model takes a workgroup's stream rate as proportional to
     a block's K + V bytes below 8 KiB (D = 128 at 16 bits), so at D = 64 the

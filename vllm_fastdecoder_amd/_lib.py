@@ -18,7 +18,7 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
-ABI_VERSION = 11
+ABI_VERSION = 12
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FD_NOALLOC_SCRATCH_BYTES of include/fdattn.h
 
 
@@ -243,6 +243,22 @@ SIGNATURES: dict[str, tuple] = {
             c_void_p, c_int32, c_int32, c_double,  # host_lens, n, block_size, cpu_fraction
             c_void_p, c_void_p, c_int64, c_void_p,  # gpu_lens, cpu_bt, cpu_bt_stride, cpu_lens
             POINTER(c_int32),                      # cpu_width
+        ],
+    ),
+    "fd_hybrid_share_start": (
+        c_int,
+        [
+            c_void_p, c_void_p, c_void_p, c_void_p,  # stream, ready_event, q, q_host
+            c_void_p, c_int64, c_int32,            # host_bt, bt_stride, bt_width
+            c_void_p, c_double,                    # host_lens, cpu_fraction
+            c_void_p, c_void_p, c_int64, c_void_p,  # gpu_lens, cpu_bt, cpu_bt_stride, cpu_lens
+            c_void_p, c_void_p,                    # k_cache, v_cache
+            c_int64, c_int64, c_int64,             # kv strides block/head/token
+            c_int64,                               # num_blocks
+            c_int32, c_int32, c_int32, c_int32,    # n, H, KVH, D
+            c_int32, c_float, c_int32,             # block_size, scale, kv_dtype
+            c_void_p, c_void_p,                    # out, lse
+            c_int32, POINTER(c_int64),             # num_threads, call
         ],
     ),
     "fd_host_store_kv": (

@@ -181,7 +181,7 @@ extern "C" {
 
 const char* fd_last_error(void) { return g_err; }
 
-int fd_abi_version(void) { return 11; }
+int fd_abi_version(void) { return 12; }
 
 int fd_paged_decode_workspace_size(int32_t n, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_size, int32_t block_size, int32_t bt_width,

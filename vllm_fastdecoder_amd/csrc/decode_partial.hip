@@ -5,6 +5,8 @@
 
 #include "decode_tiled.h"
 
+extern char** environ;  // the process environment (POSIX)
+
 namespace fd {
 
 namespace {
@@ -179,26 +181,49 @@ __global__ __launch_bounds__(kWave) void decode_generic_kernel(GenericParams p) 
   if (lane == 0) p.lse[(int64_t)h * p.lse_sh + i] = bad ? qnan() : mrun + __logf(lrun);
 }
 
-// FD_SPLIT_BLOCKS=<n> forces n blocks per task (tuning and tests).
-int split_blocks_override() {
-  const char* e = getenv("FD_SPLIT_BLOCKS");
-  return e ? atoi(e) : 0;
-}
+// The planner's tuning variables (comparison runs and tests), found in one
+// pass over the environment per plan rather than one getenv each (seven per
+// launch cost ~0.5 us of host time with ~90 variables set):
+//   FD_SPLIT_BLOCKS=<n>  n blocks per task;
+//   FD_KV_ADJ=0          separate K and V loads where V follows K;
+//   FD_DECODE_KERNEL=valu | mfma | mm  a kernel family where it applies: the
+//                        VALU kernel, the one with only the scores on the
+//                        matrix cores (4+ query heads per kv head), the one
+//                        with P.V there too (D <= 128);
+//   FD_WAVE_BLOCKS=<b>   blocks per working wave (0: every wave works);
+//   FD_WG_CAP=<k>        at most k workgroups per CU (0: no cap).
+// Like getenv, the first definition of a name counts.
+struct Tuning {
+  const char* split_blocks = nullptr;
+  const char* kv_adj = nullptr;
+  const char* kernel = nullptr;
+  const char* wave_blocks = nullptr;
+  const char* wg_cap = nullptr;
 
-// FD_KV_ADJ=0 keeps separate K and V loads where V follows K (comparison and
-// tests).
-bool kv_adj_enabled() {
-  const char* e = getenv("FD_KV_ADJ");
-  return !(e != nullptr && strcmp(e, "0") == 0);
-}
+  bool kernel_forced(const char* name) const {
+    return kernel != nullptr && strcmp(kernel, name) == 0;
+  }
+};
 
-// FD_DECODE_KERNEL=valu | mfma | mm forces a kernel family where it applies
-// (comparison and tests): the VALU kernel, the one with only the scores on
-// the matrix cores (4+ query heads per kv head), the one with P.V there too
-// (D <= 128).
-bool kernel_forced(const char* name) {
-  const char* e = getenv("FD_DECODE_KERNEL");
-  return e != nullptr && strcmp(e, name) == 0;
+Tuning read_tuning() {
+  Tuning t;
+  // the value of `entry` if it defines `name` (entry past its "FD_"), else null
+  auto value = [](const char* entry, const char* name) -> const char* {
+    const size_t k = strlen(name);
+    return strncmp(entry, name, k) == 0 && entry[k] == '=' ? entry + k + 1 : nullptr;
+  };
+  for (char** e = environ; e != nullptr && *e != nullptr; ++e) {
+    const char* s = *e;
+    if (s[0] != 'F' || s[1] != 'D' || s[2] != '_') continue;
+    s += 3;
+    const char* v;
+    if (!t.split_blocks && (v = value(s, "SPLIT_BLOCKS"))) t.split_blocks = v;
+    else if (!t.kv_adj && (v = value(s, "KV_ADJ"))) t.kv_adj = v;
+    else if (!t.kernel && (v = value(s, "DECODE_KERNEL"))) t.kernel = v;
+    else if (!t.wave_blocks && (v = value(s, "WAVE_BLOCKS"))) t.wave_blocks = v;
+    else if (!t.wg_cap && (v = value(s, "WG_CAP"))) t.wg_cap = v;
+  }
+  return t;
 }
 
 }  // namespace
@@ -484,6 +509,8 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     sp.max_splits = 1;
     return sp;
   }
+  const Tuning tune = read_tuning();
+  sp.no_kv_adj = tune.kv_adj != nullptr && strcmp(tune.kv_adj, "0") == 0;
   // tasks, splits and the model count 16-token tiles (BS / 16 per block)
   const int64_t tiles = (int64_t)(bt_width > 0 ? bt_width : 0) * (BS / kTileTokens);
   const int32_t wt = (int32_t)std::min<int64_t>(tiles, INT32_MAX);
@@ -512,14 +539,14 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
   //     groups of 5 and more. MHA at these sizes loses 5-25 % and stays on the
   //     VALU kernel. (K + V runs of 320 or 448 bytes straddle cache lines;
   //     both kernels read those sizes slower.)
-  const bool matrix_ok = matrix && !f32 && !kernel_forced("valu");
+  const bool matrix_ok = matrix && !f32 && !tune.kernel_forced("valu");
   const int cus = device_cus();
   const bool big_mha = G == 1 && D == 128 && cus > 0 && (int64_t)n * KVH >= 8LL * cus &&
                        wt >= 1024 / kTileTokens;
   const bool mm_g = D % 32 == 0 ? G >= 4 : G >= 5;
   sp.mfma = matrix_ok && G >= 4 && D == sp.kernel_d;
   sp.mm = matrix_ok && D % 16 == 0 && D >= 32 && D <= 128 &&
-          (kernel_forced("mm") || ((mm_g || big_mha) && !kernel_forced("mfma")));
+          (tune.kernel_forced("mm") || ((mm_g || big_mha) && !tune.kernel_forced("mfma")));
   if (sp.mm) {
     sp.mfma = false;
     // more than 16 heads per kv head (multi-query models): tasks of two or
@@ -529,7 +556,7 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     sp.kernel_g = 16 * cg;
   }
   sp.passes = (G + sp.kernel_g - 1) / sp.kernel_g;
-  int sb = split_blocks_override();
+  int sb = tune.split_blocks ? atoi(tune.split_blocks) : 0;
   if (sb > kMaxSplitBlocks) sb = kMaxSplitBlocks;  // 64 block ids per wave
   // each pass streams the blocks once more: count it as that many kv heads
   const int32_t kv_tasks = KVH * sp.passes;
@@ -571,10 +598,8 @@ SplitPlan plan_decode(int32_t n, int32_t H, int32_t KVH, int32_t D, int32_t BS,
     const int32_t longest = std::min(sb, wt > 0 ? wt : 1);
     sp.wave_blocks = (longest + kWavesPerTask - 1) / kWavesPerTask;
   }
-  if (const char* e = getenv("FD_WAVE_BLOCKS"))  // FD_WAVE_BLOCKS=<b>: blocks per working wave,
-    sp.wave_blocks = std::max(0, atoi(e));       // 0 every wave (tuning and tests)
-  const char* cap = getenv("FD_WG_CAP");  // FD_WG_CAP=<k>: at most k per CU, 0 none (tuning)
-  if (cap != nullptr && *cap != 0) sp.wg_cap = std::max(0, atoi(cap));
+  if (tune.wave_blocks != nullptr) sp.wave_blocks = std::max(0, atoi(tune.wave_blocks));
+  if (tune.wg_cap != nullptr && *tune.wg_cap != 0) sp.wg_cap = std::max(0, atoi(tune.wg_cap));
   return sp;
 }
 
@@ -658,7 +683,7 @@ int launch_decode(const DecodeArgs& a, const SplitPlan& sp, hipStream_t s) {
     // vLLM's cache keeps a token's V right after its K (v == k + D): the VALU
     // kernel then reads both in one load (16-bit tier 0 only; the host tier
     // of a split keeps separate K and V tensors).
-    tt.kv_adj = t == 0 && !f32 && (a.D == 128 || a.D == 256) && kv_adj_enabled() &&
+    tt.kv_adj = t == 0 && !f32 && (a.D == 128 || a.D == 256) && !sp.no_kv_adj &&
                 static_cast<const char*>(kt.v) == static_cast<const char*>(kt.k) + (int64_t)a.D * 2;
     tt.k_run_bytes = tt.run_bytes + (tt.kv_adj ? (uint32_t)a.D * 2 : 0u);
     tt.bt = kt.bt;

@@ -269,6 +269,7 @@ struct SplitPlan {
   int32_t passes;        // tasks per (sequence, kv head, block range): ceil((H / KVH) /
                          // kernel_g), each over the same blocks
   int32_t wave_blocks;   // blocks per working wave of a task (0: every wave works)
+  bool no_kv_adj;        // separate K and V loads even where V follows K (FD_KV_ADJ=0)
   int* occupancy_query;  // planner only: when set, the tiled launchers store the selected
                          // kernel's workgroups per CU there instead of launching it
 };

@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .pinned import device_ptr
+from .pinned import device_ptr, pinned_empty
 from .plan import longest_first as _longest_first
 from .plan import share_host_blocks as _share_host_blocks
 
@@ -386,66 +386,110 @@ def split_decode(
     return out, lse
 
 
+class _StagingSet:
+    """One set of the hybrid split's pinned host buffers (see _HybridStaging):
+    grow-only buffers by name, their views cached by shape and dtype (a step
+    of the same shape takes the same tensors), and the set's events."""
+
+    def __init__(self, dev_idx: int) -> None:
+        self.dev_idx = dev_idx
+        self._bufs: dict[str, torch.Tensor] = {}
+        self._views: dict[str, tuple] = {}
+        # events behind the last step's copies and reads of the buffers (a
+        # subset of release_events, which are reused step after step)
+        self.released: tuple = ()
+        self.release_events: list[torch.cuda.Event] = []
+        # timing event behind the copy of q to the host (re-recorded by each
+        # step; recorded once here so that its HIP event exists)
+        self.q_ready = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.device(dev_idx):
+            self.q_ready.record()
+        # timing event behind the GPU's launch of each step
+        self.gpu_done = torch.cuda.Event(enable_timing=True)
+
+    def view(self, name: str, shape: tuple, dtype: torch.dtype) -> torch.Tensor:
+        hit = self._views.get(name)
+        if hit is not None and hit[0] == shape and hit[1] == dtype:
+            return hit[2]
+        numel = 1
+        for d in shape:
+            numel *= int(d)
+        used = numel * dtype.itemsize
+        buf = self._bufs.get(name)
+        if buf is None or buf.numel() < max(used, 1):
+            cap = max(used, 1, 2 * (buf.numel() if buf is not None else 0))
+            # the library's mapped allocation: device_ptr finds its GPU address
+            # without asking the runtime (the merge reads the host partial there)
+            buf = pinned_empty((cap,), torch.uint8)
+            self._bufs[name] = buf
+        v = buf[:used].view(dtype).view(tuple(shape))
+        self._views[name] = (tuple(shape), dtype, v)
+        return v
+
+
 class _HybridStaging:
-    """Grow-only pinned host buffers of the hybrid split, one set per device
-    (the grow-only policy of the reference's PinnedStaging, state.py:93-124):
-    q on its way to the host cores, their fp32 partial on its way back, and
-    the host-planned index tensors on their way to the GPU. Reused every
-    step, so a step allocates no pinned memory. One hybrid step may be in
-    flight per device; the next one waits (usually not at all) until the
-    previous step's copies out of the buffers have completed."""
+    """Grow-only pinned host buffers of the hybrid split (the grow-only policy
+    of the reference's PinnedStaging, state.py:93-124): q on its way to the
+    host cores, their fp32 partial on its way back, the division of the host
+    blocks, and the host-planned index tensors on their way to the GPU.
+    Reused every step, so a step allocates no pinned memory. Two sets per
+    device, used in turn: a step's merge may still be reading its set while
+    the next step fills the other one. One hybrid step may be in flight per
+    device; a step waits (usually not at all) until the work of the step
+    before last that read or wrote its set has completed."""
 
     def __init__(self) -> None:
-        self._bufs: dict[tuple[int, str], torch.Tensor] = {}
-        self._released: dict[int, list[torch.cuda.Event]] = {}
+        self._sets: dict[tuple[int, int], _StagingSet] = {}
+        self._turn: dict[int, int] = {}
         self._pending: set[int] = set()
         self._lock = threading.Lock()
 
-    def acquire(self, dev: torch.device) -> int:
+    def acquire(self, dev: torch.device) -> _StagingSet:
         idx = dev.index if dev.index is not None else torch.cuda.current_device()
         with self._lock:
             if idx in self._pending:
                 raise RuntimeError("a hybrid split is already in flight on this device; "
                                    "finish() it before starting another")
             self._pending.add(idx)
-            evs = self._released.get(idx, ())
-        for ev in evs:
-            ev.synchronize()
-        return idx
+            slot = self._turn.get(idx, 0)
+            self._turn[idx] = slot ^ 1
+            st = self._sets.get((idx, slot))
+        if st is None:
+            try:
+                st = _StagingSet(idx)
+            except BaseException:
+                with self._lock:
+                    self._pending.discard(idx)
+                raise
+            with self._lock:
+                self._sets[(idx, slot)] = st
+        for ev in st.released:
+            if not ev.query():
+                ev.synchronize()
+        return st
 
-    def release(self, idx: int, streams) -> None:
-        """Frees device idx's buffers once the work enqueued so far on every
-        stream in `streams` (those whose copies read or write them) is done."""
+    def release(self, st: _StagingSet, streams) -> None:
+        """Frees the set once the work enqueued so far on every stream in
+        `streams` (those whose copies read or write it) is done."""
         evs = []
-        for s in dict.fromkeys(streams):  # distinct, in order
-            ev = torch.cuda.Event()
+        for k, s in enumerate(dict.fromkeys(streams)):  # distinct, in order
+            while len(st.release_events) <= k:
+                st.release_events.append(torch.cuda.Event())
+            ev = st.release_events[k]
             ev.record(s)
             evs.append(ev)
+        st.released = tuple(evs)
         with self._lock:
-            self._released[idx] = evs
-            self._pending.discard(idx)
+            self._pending.discard(st.dev_idx)
 
-    def view(self, idx: int, name: str, shape, dtype: torch.dtype) -> torch.Tensor:
-        numel = 1
-        for d in shape:
-            numel *= int(d)
-        used = numel * dtype.itemsize
-        nbytes = max(used, 1)
-        with self._lock:
-            buf = self._bufs.get((idx, name))
-            if buf is None or buf.numel() < nbytes:
-                cap = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
-                buf = torch.empty(cap, dtype=torch.uint8, pin_memory=True)
-                self._bufs[(idx, name)] = buf
-        return buf[:used].view(dtype).view(shape)
-
-    def upload(self, idx: int, name: str, t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    def upload(self, st: _StagingSet, name: str, t: torch.Tensor,
+               dev: torch.device) -> torch.Tensor:
         """A host tensor copied to the device through its pinned buffer (the
         host-side copy by numpy: single-threaded, leaving no spinning OpenMP
         team behind on the host cores)."""
         if t.is_cuda:
             return t
-        v = self.view(idx, name, t.shape, t.dtype)
+        v = st.view(name, tuple(t.shape), t.dtype)
         np.copyto(v.numpy(), t.numpy())
         return v.to(dev, non_blocking=True)
 
@@ -459,28 +503,32 @@ class HybridSplit:
     thread; finish() waits for the latter and enqueues the merge."""
 
     def __init__(self, out, lse, o_gpu=None, l_gpu=None, o_cpu=None, l_cpu=None,
-                 host_call: HostDecodeCall | None = None, q_ready=None, gpu_done=None,
-                 staging_idx=None, stream=None, owned=()):
+                 host_call: HostDecodeCall | None = None, staging: _StagingSet | None = None,
+                 stream=None, owned=()):
         self.out, self.lse = out, lse
         # those of out / lse that begin() allocated (on its stream)
         self._owned = owned
         # the staging set in use and the stream begin() enqueued its copies on
-        self._staging_idx, self._stream = staging_idx, stream
+        self._staging, self._stream = staging, stream
         self._o_gpu, self._l_gpu = o_gpu, l_gpu
         self._o_cpu, self._l_cpu = o_cpu, l_cpu
         self._call = host_call
-        # events behind the copy of q to the host and behind the GPU's launch
-        self._q_ready, self._gpu_done = q_ready, gpu_done
         self.cpu_seconds = 0.0  # time of the host cores' share (0 before finish)
         # whether the GPU's fused launch had completed when the host cores
         # finished (None before finish): the signal that balances the share
         self.gpu_finished_first: bool | None = None
+        # the merge's arguments but the stream, checked while begin() runs
+        # (the host cores' share keeps finish() off the critical path then)
+        self._merge = (_merge_args(out, o_gpu, l_gpu, o_cpu, l_cpu, lse)
+                       if o_gpu is not None else None)
 
     def _drop(self) -> None:
         # begin's uploads and the merge's reads of the host partial may sit
         # on different streams if the caller switched streams in between
-        HYBRID_STAGING.release(self._staging_idx,
-                               (self._stream, torch.cuda.current_stream(self.out.device)))
+        streams = (self._stream,)
+        if _current_stream(self._staging.dev_idx) != self._stream.cuda_stream:
+            streams += (torch.cuda.current_stream(self.out.device),)
+        HYBRID_STAGING.release(self._staging, streams)
         self._o_gpu = self._l_gpu = self._o_cpu = self._l_cpu = self._call = None
 
     def cancel(self) -> None:
@@ -500,28 +548,72 @@ class HybridSplit:
         reads that partial from the pinned staging."""
         if self._o_gpu is None:
             return self.out, self.lse
-        dev = self.out.device
         try:
             self.cpu_seconds = self._call.wait()
-            # the GPU finished first if its launch is complete now and took no
-            # longer, from q's arrival on the host, than the host cores' share
-            self.gpu_finished_first = bool(self._gpu_done.query()) and (
-                self._q_ready.elapsed_time(self._gpu_done) <= self.cpu_seconds * 1e3)
-            cur = torch.cuda.current_stream(dev)
-            if self._stream is not None and cur != self._stream:
+            cur = _current_stream(self._staging.dev_idx)
+            if cur != self._stream.cuda_stream:
                 # the GPU partial (and out / lse when begin() allocated them)
                 # came from begin's stream: keep the allocator from reusing
                 # them before this stream's merge and later work are done
                 for t in (self._o_gpu, self._l_gpu, *self._owned):
-                    t.record_stream(cur)
+                    t.record_stream(torch.cuda.current_stream(self.out.device))
             # the host partial is read by the merge straight from the pinned staging
-            merge_attn_states(self.out, self._o_gpu, self._l_gpu, self._o_cpu, self._l_cpu,
-                              out_lse=self.lse)
+            _lib.check(_lib.load_lib().fd_merge_attn_states(*self._merge, cur))
+            # the GPU finished first if its launch is complete now and took no
+            # longer, from q's arrival on the host, than the host cores' share
+            st = self._staging
+            self.gpu_finished_first = bool(st.gpu_done.query()) and (
+                st.q_ready.elapsed_time(st.gpu_done) <= self.cpu_seconds * 1e3)
         finally:
             if self._call is not None:
                 self._call.wait()  # finish interrupted: let the share stop first
             self._drop()
         return self.out, self.lse
+
+
+def _host_share_start(st: _StagingSet, stream: int, q: torch.Tensor, host_k_cache, host_v_cache,
+                      host_block_table, host_lens, softmax_scale: float, cpu_fraction: float,
+                      num_threads: int):
+    """Starts the host cores' share of a hybrid step in one library call
+    (fd_hybrid_share_start: the copy of q to the staging, its event, the
+    division of the host blocks, the queued host call). Returns the call,
+    the host partial (o, lse) and the GPU's host-tier lengths."""
+    n, H, D = q.shape
+    _require(host_k_cache.dim() == 4 and host_v_cache.shape == host_k_cache.shape
+             and host_k_cache.stride() == host_v_cache.stride() and host_k_cache.stride(3) == 1,
+             "host_k_cache/host_v_cache must be [C, KVH, BS, D], contiguous in D")
+    C, KVH, BS, Dc = host_k_cache.shape
+    _require(Dc == D and H % KVH == 0, "q must be [n, H, D] with the host cache's head size")
+    kv_dt = _dtype_code(host_k_cache, "host_k_cache")
+    _require(q.dtype == host_k_cache.dtype and host_v_cache.dtype == host_k_cache.dtype,
+             "q and the host caches must share a dtype")
+    _require(host_block_table.dim() == 2 and host_block_table.shape[0] == n
+             and host_lens.shape == (n,), "host_block_table must be [n, W] and host_lens [n]")
+    bt = host_block_table
+    if bt.dtype != torch.int32 or bt.stride(-1) != 1:
+        bt = bt.to(torch.int32).contiguous()
+    hl = host_lens
+    if hl.dtype != torch.int32 or not hl.is_contiguous():
+        hl = hl.to(torch.int32).contiguous()
+    W = bt.shape[1]
+    qc = q if q.is_contiguous() else q.contiguous()
+    q_host = st.view("q", (n, H, D), q.dtype)
+    o_cpu = st.view("o", (n, H, D), torch.float32)
+    l_cpu = st.view("lse", (H, n), torch.float32)
+    gpu_lens = st.view("gpu_lens", (n,), torch.int32)
+    cpu_lens = st.view("cpu_lens", (n,), torch.int32)
+    cpu_bt = st.view("cpu_bt", (n, max(W, 1)), torch.int32)
+    call_id = ctypes.c_int64()
+    _lib.check(_lib.load_lib().fd_hybrid_share_start(
+        stream, st.q_ready.cuda_event, qc.data_ptr(), q_host.data_ptr(),
+        bt.data_ptr(), bt.stride(0) if n else W, W, hl.data_ptr(), float(cpu_fraction),
+        gpu_lens.data_ptr(), cpu_bt.data_ptr(), cpu_bt.stride(0), cpu_lens.data_ptr(),
+        host_k_cache.data_ptr(), host_v_cache.data_ptr(),
+        host_k_cache.stride(0), host_k_cache.stride(1), host_k_cache.stride(2), C,
+        n, H, KVH, D, BS, float(softmax_scale), kv_dt,
+        o_cpu.data_ptr(), l_cpu.data_ptr(), int(num_threads), ctypes.byref(call_id)))
+    keep = (qc, host_k_cache, host_v_cache, bt, hl)
+    return HostDecodeCall(call_id.value or None, keep), o_cpu, l_cpu, gpu_lens
 
 
 def hybrid_split_begin(
@@ -542,14 +634,15 @@ def hybrid_split_begin(
     hbm_lens_dev: torch.Tensor | None = None,
     host_block_table_dev: torch.Tensor | None = None,
 ) -> HybridSplit:
-    """First half of hybrid_split_decode: divides the host tier, starts the
-    copy of q to the host and queues the host cores' share behind it on the
-    library's runner thread (it starts as soon as q is on the host), then
-    enqueues the GPU's fused launch. Other GPU work can be enqueued before
-    HybridSplit.finish(), which waits for the host cores and enqueues the
-    merge. hbm_lens_dev / host_block_table_dev: device copies of hbm_lens /
-    host_block_table the caller already holds (the GPU's share reads the host
-    table unchanged, only with shorter lengths), saving their uploads."""
+    """First half of hybrid_split_decode: starts the copy of q to the host,
+    divides the host tier and queues the host cores' share behind the copy on
+    the library's runner thread (it starts as soon as q is on the host; all
+    three in one library call), then enqueues the GPU's fused launch. Other
+    GPU work can be enqueued before HybridSplit.finish(), which waits for the
+    host cores and enqueues the merge. hbm_lens_dev / host_block_table_dev:
+    device copies of hbm_lens / host_block_table the caller already holds
+    (the GPU's share reads the host table unchanged, only with shorter
+    lengths), saving their uploads."""
     _require(q.is_cuda and q.dim() == 3, "q must be [n, H, D] on the GPU")
     _require(host_block_table.device.type == "cpu" and host_lens.device.type == "cpu",
              "host_block_table and host_lens must be CPU tensors")
@@ -567,31 +660,24 @@ def hybrid_split_begin(
     if n == 0:
         _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2], cpu_fraction)
         return HybridSplit(out, lse)
-    stream = torch.cuda.current_stream(dev)
-    idx = HYBRID_STAGING.acquire(dev)
+    st = HYBRID_STAGING.acquire(dev)
+    stream = None
     call = None
     try:
-        # q on its way to the host first: the copy overlaps the share's host work
-        q_host = HYBRID_STAGING.view(idx, "q", q.shape, q.dtype)
-        q_host.copy_(q, non_blocking=True)
-        q_ready = torch.cuda.Event(enable_timing=True)
-        q_ready.record(stream)
-        share = _share_host_blocks(host_block_table, host_lens, host_k_cache.shape[2],
-                                   cpu_fraction)
-        o_cpu = HYBRID_STAGING.view(idx, "o", (n, H, D), torch.float32)
-        l_cpu = HYBRID_STAGING.view(idx, "lse", (H, n), torch.float32)
-        # the host cores' blocks, from when q is on the host
-        call = host_decode_start(q_host, host_k_cache, host_v_cache, share.cpu_bt,
-                                 share.cpu_lens, softmax_scale, o_cpu, l_cpu,
-                                 num_threads=num_threads, ready=q_ready)
+        # the host cores' share first: it is the step's longer half (the
+        # stream's torch object, slower to get, only once it is queued)
+        call, o_cpu, l_cpu, gpu_lens = _host_share_start(
+            st, _current_stream(st.dev_idx), q, host_k_cache, host_v_cache, host_block_table,
+            host_lens, softmax_scale, cpu_fraction, num_threads)
+        stream = torch.cuda.current_stream(dev)
 
         def up(name, t):  # host index tensors: through pinned staging, asynchronous
-            return HYBRID_STAGING.upload(idx, name, t, dev)
+            return HYBRID_STAGING.upload(st, name, t, dev)
 
         # rows by decreasing GPU work when the HBM lengths are known on the host
         order = None
         if not hbm_lens.is_cuda:
-            work = hbm_lens.numpy().astype(np.int64) + share.gpu_lens.numpy()
+            work = hbm_lens.numpy().astype(np.int64) + gpu_lens.numpy()
             order = up("order", torch.from_numpy(
                 np.argsort(-work, kind="stable").astype(np.int32)))
         o_gpu = torch.empty(n, H, D, dtype=torch.float32, device=dev)
@@ -599,20 +685,21 @@ def hybrid_split_begin(
         hl = hbm_lens_dev if hbm_lens_dev is not None else up("hbm_lens", hbm_lens)
         hbt = (host_block_table_dev if host_block_table_dev is not None
                else up("host_bt", host_block_table))
+        # the GPU's host-tier lengths are already in pinned staging
         split_decode(q, hbm_key_cache, hbm_value_cache, up("hbm_bt", hbm_block_table), hl,
-                     host_k_cache, host_v_cache, hbt, up("gpu_lens", share.gpu_lens),
+                     host_k_cache, host_v_cache, hbt, gpu_lens.to(dev, non_blocking=True),
                      softmax_scale, out=o_gpu, lse=l_gpu, row_order=order)
-        gpu_done = torch.cuda.Event(enable_timing=True)
-        gpu_done.record(stream)
+        st.gpu_done.record(stream)
+        h = HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, call, staging=st, stream=stream,
+                        owned=tuple(owned))
     except BaseException:
         try:
             if call is not None:
                 call.wait()  # the share reads the staging: let it stop first
         finally:
-            HYBRID_STAGING.release(idx, (stream,))
+            HYBRID_STAGING.release(st, (stream or torch.cuda.current_stream(dev),))
         raise
-    return HybridSplit(out, lse, o_gpu, l_gpu, o_cpu, l_cpu, call, q_ready, gpu_done,
-                       staging_idx=idx, stream=stream, owned=tuple(owned))
+    return h
 
 
 def hybrid_split_decode(
@@ -895,6 +982,12 @@ def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
     used at fastdecode/backend.py:53-55 (rule of cpu_ops.py:93-113). o_b /
     lse_b may also be views of pinned host memory (the host cores' partial):
     the merge then reads them zero-copy over the link."""
+    _lib.check(_lib.load_lib().fd_merge_attn_states(
+        *_merge_args(out, o_a, lse_a, o_b, lse_b, out_lse), _stream_for(out)))
+
+
+def _merge_args(out, o_a, lse_a, o_b, lse_b, out_lse) -> tuple:
+    """fd_merge_attn_states' arguments but the stream, after the checks."""
     _require(out.dim() == 3 and o_a.shape == out.shape and o_b.shape == out.shape,
              "out, o_a, o_b must be [n, H, D] of one shape")
     n, H, D = out.shape
@@ -909,19 +1002,14 @@ def merge_attn_states(out, o_a, lse_a, o_b, lse_b, out_lse=None) -> None:
     if out_lse is not None:
         _require(out_lse.dtype == torch.float32 and tuple(out_lse.shape) == (H, n) and
                  (n == 0 or out_lse.stride(1) == 1), "out_lse must be float32 [H, n]")
-    _lib.check(
-        _lib.load_lib().fd_merge_attn_states(
-            out.data_ptr(), out.stride(0), out.stride(1), _dtype_code(out, "out"),
+    return (out.data_ptr(), out.stride(0), out.stride(1), _dtype_code(out, "out"),
             o_a.data_ptr(), o_a.stride(0), o_a.stride(1), _dtype_code(o_a, "o_a"),
             lse_a.data_ptr(), lse_a.stride(0),
             device_ptr(o_b), o_b.stride(0), o_b.stride(1), _dtype_code(o_b, "o_b"),
             device_ptr(lse_b), lse_b.stride(0),
             out_lse.data_ptr() if out_lse is not None else None,
             out_lse.stride(0) if out_lse is not None else 0,
-            n, H, D,
-            _stream_for(out),
-        )
-    )
+            n, H, D)
 
 
 def _device_counter(t, what):
