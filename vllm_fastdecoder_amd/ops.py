@@ -454,18 +454,18 @@ class _HybridStaging:
             slot = self._turn.get(idx, 0)
             self._turn[idx] = slot ^ 1
             st = self._sets.get((idx, slot))
-        if st is None:
-            try:
+        try:
+            if st is None:
                 st = _StagingSet(idx)
-            except BaseException:
                 with self._lock:
-                    self._pending.discard(idx)
-                raise
+                    self._sets[(idx, slot)] = st
+            for ev in st.released:
+                if not ev.query():
+                    ev.synchronize()
+        except BaseException:  # the device stays free for the next split
             with self._lock:
-                self._sets[(idx, slot)] = st
-        for ev in st.released:
-            if not ev.query():
-                ev.synchronize()
+                self._pending.discard(idx)
+            raise
         return st
 
     def release(self, st: _StagingSet, streams) -> None:
