@@ -559,8 +559,9 @@ int fd_share_host_blocks(const int32_t* host_bt, int64_t bt_stride, int32_t bt_w
  *      [n, H, D], contiguous) and lse (fp32 [H, n], contiguous) behind
  *      ready_event, and returns at once with *call for fd_host_decode_wait.
  * The arguments are checked first (an invalid call enqueues and queues
- * nothing); a table row needing more than bt_width blocks fails in step 2,
- * after the copy was enqueued, and queues no call. n = 0: nothing is done
+ * nothing; host_bt may be NULL when bt_width is 0); a table row needing
+ * more than bt_width blocks fails in step 2, after the copy was enqueued,
+ * and queues no call. n = 0: nothing is done
  * and *call = 0 (nothing to wait for). Replaces the copy, the share and the
  * start that a caller would otherwise make one by one, which cost the step
  * ~0.1 ms of host time between the host cores' shares. */

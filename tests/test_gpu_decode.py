@@ -220,6 +220,12 @@ def test_all_empty_and_zero_rows(gpu):
     # n == 0 is a no-op
     ops.decode_attn(q[:0].to(gpu), kc.to(gpu), vc.to(gpu), bt[:0].to(gpu), lens[:0].to(gpu), 0.1,
                     out[:0], lse[:, :0])
+    # a table of no columns: empty rows stay empty, a row with tokens is a
+    # range error (NaN), nothing of the table is read
+    lens_w0 = torch.tensor([0, 5, 0], dtype=torch.int32)
+    out, lse = run_host_layout(q, kc, vc, bt[:, :0], lens_w0, 0.125, torch.bfloat16, gpu)
+    assert torch.all(out[[0, 2]] == 0) and torch.all(torch.isneginf(lse[:, [0, 2]]))
+    assert torch.isnan(out[1]).all() and torch.isnan(lse[:, 1]).all()
 
 
 def test_invalid_arguments_raise_before_writing(gpu):

@@ -117,6 +117,35 @@ def test_back_to_back_steps_over_both_staging_sets(gpu):
         check(out, lse, ref_o, ref_l, c["lens"])
 
 
+@pytest.mark.parametrize("width", [0, 3])
+def test_hybrid_with_an_empty_host_tier(gpu, width):
+    """No row has host-tier tokens (a zero-width host table, or zero lengths
+    in a padded one): the host cores' share is all empty rows, and the step
+    equals the HBM-tier partial alone."""
+    c = two_tier_case(8, 16, 4, 64, torch.float16, seed=21, dev=gpu, special=False)
+    q = c["q"].to(gpu)
+    n, H, D = q.shape
+    nb_g = (c["len_g"] + 15) // 16
+    len_g = nb_g * 16  # whole HBM blocks: the HBM tier holds every token here
+    c["len_g"] = len_g.to(torch.int32)
+    c["len_c"] = torch.zeros(n, dtype=torch.int32)
+    c["bt_c"] = torch.zeros(n, width, dtype=torch.int32)
+    out = torch.empty(n, H, D, dtype=torch.float32, device=gpu)
+    lse = torch.empty(H, n, dtype=torch.float32, device=gpu)
+    for frac in (0.0, 0.5, 1.0):
+        ops.hybrid_split_decode(q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"],
+                                c["hk"], c["hv"], c["bt_c"], c["len_c"], c["scale"], frac,
+                                out=out, lse=lse)
+        ref_o, ref_l = ops.paged_decode(q, c["kv"][..., :D], c["kv"][..., D:],
+                                        c["bt_g"].to(gpu), c["len_g"].to(gpu), c["scale"],
+                                        out=torch.empty_like(out))
+        torch.cuda.synchronize()
+        nz = c["len_g"] > 0
+        assert float((out[nz.to(gpu)] - ref_o[nz.to(gpu)]).abs().max()) <= 2e-5, frac
+        assert float((lse[:, nz.to(gpu)] - ref_l[:, nz.to(gpu)]).abs().max()) <= 2e-5, frac
+        assert torch.all(out[~nz.to(gpu)] == 0) and torch.all(torch.isneginf(lse[:, ~nz.to(gpu)]))
+
+
 def test_hybrid_sees_kv_written_by_the_gpu(gpu):
     """The step's new token is written into the pinned host tier by the GPU
     (reshape_and_cache on the stream) and then read by the host cores."""

@@ -213,8 +213,8 @@ int fd_hybrid_share_start(
   if (!(cpu_fraction >= 0.0 && cpu_fraction <= 1.0))
     return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: cpu_fraction must be in [0, 1]");
   if (n == 0) return FD_OK;
-  if (q == nullptr || ready_event == nullptr || host_bt == nullptr || host_lens == nullptr ||
-      gpu_lens == nullptr)
+  if (q == nullptr || ready_event == nullptr || (bt_width > 0 && host_bt == nullptr) ||
+      host_lens == nullptr || gpu_lens == nullptr)
     return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: NULL pointer");
   if (bt_stride < bt_width || cpu_bt_stride < std::max<int32_t>(bt_width, 1))
     return set_error(FD_ERR_INVALID,

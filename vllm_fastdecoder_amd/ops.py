@@ -67,6 +67,19 @@ def _on_device(t: torch.Tensor, device: torch.device) -> torch.Tensor:
     return t.to(device, non_blocking=False)
 
 
+def _table_on_device(bt: torch.Tensor, device: torch.device) -> tuple[torch.Tensor, int]:
+    """A block table on the device and the pointer to pass for it. A table of
+    no columns is passed as a one-id stand-in buffer (returned to keep it
+    alive) with width 0: the library takes no NULL table, reads nothing of a
+    zero-width one, and treats any row with tokens as a range error (NaN
+    row)."""
+    if bt.shape[1] == 0:
+        hold = torch.zeros(1, dtype=torch.int32, device=device)
+        return hold, hold.data_ptr()
+    t = _on_device(bt, device)
+    return t, t.data_ptr()
+
+
 class _Workspace:
     """Grow-only device scratch for the split partials (the same grow-only
     policy as the reference's PinnedStaging.get, state.py:115-124), one
@@ -242,11 +255,11 @@ def paged_decode_partial(
     if n == 0:
         return
     dev = q.device
-    bt = _on_device(block_table, dev)
+    W = block_table.shape[1]
+    bt, bt_ptr = _table_on_device(block_table, dev)
     ln = _on_device(lens, dev)
-    _require(bt.stride(1) == 1, "block_table rows must be contiguous")
+    _require(W == 0 or bt.stride(1) == 1, "block_table rows must be contiguous")
     ln = ln.contiguous()
-    W = bt.shape[1]
     need = workspace_bytes(n, H, num_kv_heads, D, block_size, W)
     if workspace is None:
         workspace = WORKSPACE.get(dev, need)
@@ -264,7 +277,7 @@ def paged_decode_partial(
         device_ptr(k_cache), device_ptr(v_cache),
         kv_strides[0], kv_strides[1], kv_strides[2],
         num_blocks,
-        bt.data_ptr(), bt.stride(0), W,
+        bt_ptr, bt.stride(0) if W else 0, W,
         ln.data_ptr(), order_ptr,
         n, H, num_kv_heads, D,
         block_size, float(scale), kv_dt,
@@ -295,12 +308,13 @@ def _tier(k_cache, v_cache, strides, num_blocks, block_table, lens, n, dev, what
     _require(k_cache.stride() == v_cache.stride() and k_cache.shape == v_cache.shape,
              f"{what}: k and v caches must share shape and strides")
     _require(k_cache.stride(-1) == 1, f"{what}: caches must be contiguous in head_size")
-    bt = _on_device(block_table, dev)
-    _require(bt.stride(1) == 1 or bt.shape[1] <= 1, f"{what}: block_table rows must be contiguous")
+    W = block_table.shape[1]
+    bt, bt_ptr = _table_on_device(block_table, dev)
+    _require(W <= 1 or bt.stride(1) == 1, f"{what}: block_table rows must be contiguous")
     ln = _on_device(lens, dev).contiguous()
     desc = _lib.FdKvTier(
         device_ptr(k_cache), device_ptr(v_cache), strides[0], strides[1], strides[2], num_blocks,
-        bt.data_ptr(), bt.stride(0), bt.shape[1], ln.data_ptr(),
+        bt_ptr, bt.stride(0) if W else 0, W, ln.data_ptr(),
     )
     return desc, (bt, ln)
 
