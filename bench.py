@@ -899,7 +899,10 @@ def main() -> int:
     }
     torch.cuda.empty_cache()
     if not args.no_split_run and w.name in ("vicuna7b", "llama3_8b"):
-        result["split_run"] = split_run(w, lens, bt, q, args.steps, args.warmup, stream)
+        try:
+            result["split_run"] = split_run(w, lens, bt, q, args.steps, args.warmup, stream)
+        except Exception as e:  # e.g. no room for the pinned host tier: keep the line
+            result["split_run"] = {"error": f"{type(e).__name__}: {e}"}
         torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, lens, bt, pool, q.cpu(), args.cpu_iters)
