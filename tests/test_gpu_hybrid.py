@@ -117,6 +117,25 @@ def test_back_to_back_steps_over_both_staging_sets(gpu):
         check(out, lse, ref_o, ref_l, c["lens"])
 
 
+def test_a_refused_step_leaves_the_next_one_working(gpu):
+    """A host row needing more blocks than its table holds is refused by the
+    library after q's copy was enqueued: begin() raises, queues no host call,
+    frees its staging set, and the next steps (on both sets) run normally."""
+    c = two_tier_case(6, 8, 2, 64, torch.float16, seed=31, dev=gpu)
+    q = c["q"].to(gpu)
+    D = q.shape[2]
+    bad_lens = c["len_c"].clone()
+    bad_lens[3] = c["bt_c"].shape[1] * 16 + 1
+    args = (q, c["kv"][..., :D], c["kv"][..., D:], c["bt_g"], c["len_g"], c["hk"], c["hv"],
+            c["bt_c"])
+    with pytest.raises(RuntimeError, match="needs .* blocks"):
+        ops.hybrid_split_begin(*args, bad_lens, c["scale"], 0.5)
+    ref_o, ref_l = oracle_merged(c)
+    for _ in range(3):
+        out, lse = run_hybrid(c, gpu, 0.5)
+        check(out, lse, ref_o, ref_l, c["lens"])
+
+
 @pytest.mark.parametrize("width", [0, 3])
 def test_hybrid_with_an_empty_host_tier(gpu, width):
     """No row has host-tier tokens (a zero-width host table, or zero lengths
