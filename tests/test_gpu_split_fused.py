@@ -245,6 +245,39 @@ def test_fused_range_errors_poison_only_their_rows(gpu):
     check_vs_oracle(out, lse, ref, ref_lse, ok)
 
 
+def test_fused_with_a_zero_width_tier(gpu):
+    """Every row in one tier: the other tier's table has no columns (and its
+    lengths are 0). The fused launch equals the oracle of the tier that holds
+    the rows; a row given tokens in the empty tier is a range error (NaN)."""
+    for hbm_only in (True, False):
+        c = two_tier_case(5, 16, 4, 64, torch.float16, seed=12 + hbm_only, dev=gpu,
+                          special=False)
+        n = c["q"].shape[0]
+        t = dict(c)
+        if hbm_only:  # whole-block HBM rows: give each its host blocks' count in HBM ids
+            t["len_g"] = ((c["len_g"] + 15) // 16 * 16).to(torch.int32)
+            t["len_c"] = torch.zeros(n, dtype=torch.int32)
+            t["bt_c"] = torch.zeros(n, 0, dtype=torch.int32)
+        else:
+            t["len_g"] = torch.zeros(n, dtype=torch.int32)
+            t["bt_g"] = torch.zeros(n, 0, dtype=torch.int32)
+        out, lse = run_fused(c, gpu, tiers=t)
+        ref, ref_lse = oracle_merged(dict(c, **{k: t[k] for k in ("len_g", "len_c")},
+                                          bt_g=t["bt_g"] if t["bt_g"].shape[1] else
+                                          torch.zeros(n, 1, dtype=torch.int32),
+                                          bt_c=t["bt_c"] if t["bt_c"].shape[1] else
+                                          torch.zeros(n, 1, dtype=torch.int32)))
+        nz = (t["len_g"] + t["len_c"]) > 0
+        check_vs_oracle(out, lse, ref, ref_lse, nz)
+        assert torch.all(out.cpu()[~nz] == 0) and torch.all(torch.isneginf(lse.cpu()[:, ~nz]))
+        bad = dict(t)
+        key = "len_c" if hbm_only else "len_g"
+        bad[key] = t[key].clone()
+        bad[key][1] = 3
+        out, lse = run_fused(c, gpu, tiers=bad)
+        assert torch.isnan(out[1]).all() and torch.isnan(lse[:, 1]).all()
+
+
 def test_fused_rejects_mismatched_tiers(gpu):
     c = two_tier_case(2, 8, 8, 64, torch.float16, seed=1, dev=gpu, hi=200, special=False)
     q = c["q"].to(gpu)
