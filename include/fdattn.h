@@ -603,9 +603,11 @@ int fd_host_decode_isa(void);
 
 /* Measurement helper: reads `bytes` (a multiple of 64) of host memory at src
  * (64-byte aligned) on num_threads host cores (0: as fd_host_decode_partial
- * picks them), with no work per byte beyond an XOR into *checksum (the XOR
- * of all 64-bit words). Its rate is what the host cores can stream from
- * DRAM: the bound of the host-core leg of the split step. No counterpart in
+ * picks them), in 1 MiB pieces streamed with prefetched 32-byte loads (the
+ * way the host-core kernel reads its blocks), with no work per byte beyond
+ * an XOR into *checksum (the XOR of all 64-bit words). Its rate is what the
+ * host cores can stream from DRAM: the bound of the host-core leg of the
+ * split step. No counterpart in
  * the reference, whose README bounds the CPU side by the host's memory
  * bandwidth (README.md:86-87). */
 int fd_host_stream_read(const void* src, size_t bytes, int32_t num_threads, uint64_t* checksum);

@@ -388,6 +388,42 @@ struct V : isa_avx512::V512 {
 }  // namespace isa_avx512bf16
 #pragma GCC pop_options
 
+// ------------------------------------------------ plain streaming read (measurement)
+#pragma GCC push_options
+#pragma GCC target("avx2")
+namespace read_avx2 {
+
+// XOR of the 64-bit words in bytes [lo, hi) of p (64-byte aligned, hi - lo a
+// multiple of 64), read with 32-byte loads into four independent chains, each
+// 64-byte line prefetched kAhead bytes before its load (the host-core kernel
+// prefetches its next block runs the same way: the hardware prefetchers
+// alone leave the cores' DRAM streams short of their rate).
+uint64_t xor_lines(const char* p, size_t lo, size_t hi) {
+  constexpr size_t kAhead = 2048;
+  __m256i a = _mm256_setzero_si256(), b = a, c = a, d = a;
+  size_t o = lo;
+  for (; o + 128 <= hi; o += 128) {
+    if (o + kAhead + 128 <= hi) {
+      _mm_prefetch(p + o + kAhead, _MM_HINT_T0);
+      _mm_prefetch(p + o + kAhead + 64, _MM_HINT_T0);
+    }
+    a = _mm256_xor_si256(a, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o)));
+    b = _mm256_xor_si256(b, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 32)));
+    c = _mm256_xor_si256(c, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 64)));
+    d = _mm256_xor_si256(d, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 96)));
+  }
+  if (o < hi) {  // a last 64-byte line
+    a = _mm256_xor_si256(a, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o)));
+    b = _mm256_xor_si256(b, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 32)));
+  }
+  const __m256i x = _mm256_xor_si256(_mm256_xor_si256(a, b), _mm256_xor_si256(c, d));
+  return (uint64_t)_mm256_extract_epi64(x, 0) ^ (uint64_t)_mm256_extract_epi64(x, 1) ^
+         (uint64_t)_mm256_extract_epi64(x, 2) ^ (uint64_t)_mm256_extract_epi64(x, 3);
+}
+
+}  // namespace read_avx2
+#pragma GCC pop_options
+
 // Vector width the kernel uses on this CPU: 512 (AVX-512F) or 256 (AVX2),
 // 0 if neither is available. FASTDECODE_CPU_ISA=avx2 keeps to AVX2.
 int isa_bits() {
@@ -554,9 +590,10 @@ extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 
 // Plain multi-threaded read of a host buffer on the pool that runs the
 // host-core kernel: 1 MiB chunks handed out from an atomic counter, each
-// read as 64-bit words into eight independent XOR chains (no other work per
-// byte), so the rate is the cores' DRAM read rate for a streamed buffer. The
-// XOR of all words comes back as a checksum (order independent).
+// streamed with prefetched 32-byte loads into XOR chains (no other work per
+// byte; 64-bit words where AVX2 is missing), so the rate is the cores' DRAM
+// read rate for a streamed buffer. The XOR of all words comes back as a
+// checksum (order independent).
 extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_threads,
                                    uint64_t* checksum) {
   if (bytes % 64 != 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
@@ -573,6 +610,7 @@ extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_th
   std::atomic<int64_t> next{0};
   std::atomic<uint64_t> total{0};
   const uint64_t* words = static_cast<const uint64_t*>(src);
+  const bool avx2 = isa_bits() != 0;
   PoolState& ps = pool_state();
   std::lock_guard<std::mutex> call(ps.call_mu);
   ps.pool.run(nt, [&](int) {
@@ -580,9 +618,13 @@ extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_th
     for (;;) {
       const int64_t c = next.fetch_add(1, std::memory_order_relaxed);
       if (c >= chunks) break;
-      const size_t lo = (size_t)c * kChunk / 8;
-      const size_t hi = std::min(bytes, (size_t)(c + 1) * kChunk) / 8;
-      for (size_t w = lo; w < hi; w += 8)
+      const size_t lo = (size_t)c * kChunk;
+      const size_t hi = std::min(bytes, (size_t)(c + 1) * kChunk);
+      if (avx2) {
+        x[0] ^= read_avx2::xor_lines(static_cast<const char*>(src), lo, hi);
+        continue;
+      }
+      for (size_t w = lo / 8; w < hi / 8; w += 8)
         for (int j = 0; j < 8; ++j) x[j] ^= words[w + j];
     }
     total.fetch_xor(x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7],
