@@ -60,7 +60,8 @@ enum fd_status {
   FD_ERR_RANGE = 2,       /* slot or block id outside the cache */
   FD_ERR_WORKSPACE = 3,   /* workspace missing or too small */
   FD_ERR_HIP = 4,         /* a HIP runtime call failed */
-  FD_ERR_UNSUPPORTED = 5  /* valid but not implemented (e.g. head_size) */
+  FD_ERR_UNSUPPORTED = 5, /* valid but not implemented (e.g. head_size) */
+  FD_ERR_RESOURCE = 6     /* the host ran out of memory or threads */
 };
 
 /* Message describing the last failed call on this host thread

@@ -18,6 +18,7 @@ from .build import LIB_PATH
 FD_F16, FD_BF16, FD_F32 = 0, 1, 2
 FD_OK = 0
 FD_ERR_INVALID, FD_ERR_RANGE, FD_ERR_WORKSPACE, FD_ERR_HIP, FD_ERR_UNSUPPORTED = 1, 2, 3, 4, 5
+FD_ERR_RESOURCE = 6
 ABI_VERSION = 12
 NOALLOC_SCRATCH_BYTES = 32 << 20  # FD_NOALLOC_SCRATCH_BYTES of include/fdattn.h
 

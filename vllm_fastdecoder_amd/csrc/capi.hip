@@ -478,9 +478,16 @@ int fd_host_alloc(size_t bytes, void** host_ptr) {
   if (nc != nullptr && nc[0] == '1') flags |= hipHostMallocNonCoherent;
   e = hipHostMalloc(host_ptr, bytes, flags);
   if (e != hipSuccess) return hip_error(e, "hipHostMalloc");
-  std::lock_guard<std::mutex> lock(g_host_mu);
-  host_blocks()[*host_ptr] = dev;
-  return FD_OK;
+  const int rc = guarded("host_alloc", [&]() -> int {
+    std::lock_guard<std::mutex> lock(g_host_mu);
+    host_blocks()[*host_ptr] = dev;
+    return FD_OK;
+  });
+  if (rc != FD_OK) {  // not recorded (no memory for the entry): give the block back
+    (void)hipHostFree(*host_ptr);
+    *host_ptr = nullptr;
+  }
+  return rc;
 }
 
 int fd_host_free(void* host_ptr) {

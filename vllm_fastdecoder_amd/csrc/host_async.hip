@@ -178,22 +178,26 @@ int fd_host_decode_partial_start(
     int32_t head_size, int32_t block_size, float scale, int32_t kv_dtype, void* out,
     int64_t out_stride_seq, int64_t out_stride_head, int32_t out_dtype, float* lse,
     int64_t lse_stride_head, int32_t num_threads, int64_t* call) {
-  if (call == nullptr)
-    return set_error(FD_ERR_INVALID, "fd_host_decode_partial_start: call is NULL");
-  const int rc = host_decode_check(q, k_cache, v_cache, num_blocks, block_table, bt_stride,
-                                   bt_width, lens, n, num_heads, num_kv_heads, head_size,
-                                   block_size, scale, kv_dtype, out, out_dtype, lse, num_threads);
-  if (rc != FD_OK) return rc;
-  HostCall c{0, static_cast<hipEvent_t>(ready_event), q, q_stride_seq, q_stride_head, k_cache,
-             v_cache, kv_stride_block, kv_stride_head, kv_stride_token, num_blocks, block_table,
-             bt_stride, bt_width, lens, n, num_heads, num_kv_heads, head_size, block_size, scale,
-             kv_dtype, out, out_stride_seq, out_stride_head, out_dtype, lse, lse_stride_head,
-             num_threads};
-  *call = runner().submit(c);
-  return FD_OK;
+  return guarded("fd_host_decode_partial_start", [&]() -> int {
+    if (call == nullptr)
+      return set_error(FD_ERR_INVALID, "fd_host_decode_partial_start: call is NULL");
+    const int rc = host_decode_check(q, k_cache, v_cache, num_blocks, block_table, bt_stride,
+                                     bt_width, lens, n, num_heads, num_kv_heads, head_size,
+                                     block_size, scale, kv_dtype, out, out_dtype, lse, num_threads);
+    if (rc != FD_OK) return rc;
+    HostCall c{0, static_cast<hipEvent_t>(ready_event), q, q_stride_seq, q_stride_head, k_cache,
+               v_cache, kv_stride_block, kv_stride_head, kv_stride_token, num_blocks, block_table,
+               bt_stride, bt_width, lens, n, num_heads, num_kv_heads, head_size, block_size, scale,
+               kv_dtype, out, out_stride_seq, out_stride_head, out_dtype, lse, lse_stride_head,
+               num_threads};
+    *call = runner().submit(c);
+    return FD_OK;
+  });
 }
 
-int fd_host_decode_wait(int64_t call, double* seconds) { return runner().wait(call, seconds); }
+int fd_host_decode_wait(int64_t call, double* seconds) {
+  return guarded("fd_host_decode_wait", [&]() -> int { return runner().wait(call, seconds); });
+}
 
 int fd_hybrid_share_start(
     void* stream, void* ready_event, const void* q, void* q_host, const int32_t* host_bt,
@@ -203,40 +207,42 @@ int fd_hybrid_share_start(
     int64_t kv_stride_token, int64_t num_blocks, int32_t n, int32_t num_heads,
     int32_t num_kv_heads, int32_t head_size, int32_t block_size, float scale, int32_t kv_dtype,
     float* out, float* lse, int32_t num_threads, int64_t* call) {
-  if (call == nullptr) return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: call is NULL");
-  *call = 0;
-  // the host call's checks, on the buffers it will read and write
-  int rc = host_decode_check(q_host, k_cache, v_cache, num_blocks, cpu_bt, cpu_bt_stride,
-                             bt_width, cpu_lens, n, num_heads, num_kv_heads, head_size,
-                             block_size, scale, kv_dtype, out, FD_F32, lse, num_threads);
-  if (rc != FD_OK) return rc;
-  if (!(cpu_fraction >= 0.0 && cpu_fraction <= 1.0))
-    return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: cpu_fraction must be in [0, 1]");
-  if (n == 0) return FD_OK;
-  if (q == nullptr || ready_event == nullptr || (bt_width > 0 && host_bt == nullptr) ||
-      host_lens == nullptr || gpu_lens == nullptr)
-    return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: NULL pointer");
-  if (bt_stride < bt_width || cpu_bt_stride < std::max<int32_t>(bt_width, 1))
-    return set_error(FD_ERR_INVALID,
-                     "fd_hybrid_share_start: a table's row stride is below its width");
-  // q on its way to the host first: the copy overlaps the share below
-  const size_t elt = kv_dtype == FD_F32 ? 4 : 2;
-  const int64_t row = (int64_t)num_heads * head_size;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e = hipMemcpyAsync(q_host, q, (size_t)n * row * elt, hipMemcpyDeviceToHost, s);
-  if (e != hipSuccess) return hip_error(e, "fd_hybrid_share_start: copy of q to the host");
-  e = hipEventRecord(static_cast<hipEvent_t>(ready_event), s);
-  if (e != hipSuccess) return hip_error(e, "fd_hybrid_share_start: hipEventRecord");
-  int32_t width = 0;
-  rc = fd_share_host_blocks(host_bt, bt_stride, bt_width, host_lens, n, block_size,
-                            cpu_fraction, gpu_lens, cpu_bt, cpu_bt_stride, cpu_lens, &width);
-  if (rc != FD_OK) return rc;
-  HostCall c{0, static_cast<hipEvent_t>(ready_event), q_host, row, head_size, k_cache, v_cache,
-             kv_stride_block, kv_stride_head, kv_stride_token, num_blocks, cpu_bt, cpu_bt_stride,
-             std::max<int32_t>(width, 1), cpu_lens, n, num_heads, num_kv_heads, head_size,
-             block_size, scale, kv_dtype, out, row, head_size, FD_F32, lse, n, num_threads};
-  *call = runner().submit(c);
-  return FD_OK;
+  return guarded("fd_hybrid_share_start", [&]() -> int {
+    if (call == nullptr) return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: call is NULL");
+    *call = 0;
+    // the host call's checks, on the buffers it will read and write
+    int rc = host_decode_check(q_host, k_cache, v_cache, num_blocks, cpu_bt, cpu_bt_stride,
+                               bt_width, cpu_lens, n, num_heads, num_kv_heads, head_size,
+                               block_size, scale, kv_dtype, out, FD_F32, lse, num_threads);
+    if (rc != FD_OK) return rc;
+    if (!(cpu_fraction >= 0.0 && cpu_fraction <= 1.0))
+      return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: cpu_fraction must be in [0, 1]");
+    if (n == 0) return FD_OK;
+    if (q == nullptr || ready_event == nullptr || (bt_width > 0 && host_bt == nullptr) ||
+        host_lens == nullptr || gpu_lens == nullptr)
+      return set_error(FD_ERR_INVALID, "fd_hybrid_share_start: NULL pointer");
+    if (bt_stride < bt_width || cpu_bt_stride < std::max<int32_t>(bt_width, 1))
+      return set_error(FD_ERR_INVALID,
+                       "fd_hybrid_share_start: a table's row stride is below its width");
+    // q on its way to the host first: the copy overlaps the share below
+    const size_t elt = kv_dtype == FD_F32 ? 4 : 2;
+    const int64_t row = (int64_t)num_heads * head_size;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(q_host, q, (size_t)n * row * elt, hipMemcpyDeviceToHost, s);
+    if (e != hipSuccess) return hip_error(e, "fd_hybrid_share_start: copy of q to the host");
+    e = hipEventRecord(static_cast<hipEvent_t>(ready_event), s);
+    if (e != hipSuccess) return hip_error(e, "fd_hybrid_share_start: hipEventRecord");
+    int32_t width = 0;
+    rc = fd_share_host_blocks(host_bt, bt_stride, bt_width, host_lens, n, block_size,
+                              cpu_fraction, gpu_lens, cpu_bt, cpu_bt_stride, cpu_lens, &width);
+    if (rc != FD_OK) return rc;
+    HostCall c{0, static_cast<hipEvent_t>(ready_event), q_host, row, head_size, k_cache, v_cache,
+               kv_stride_block, kv_stride_head, kv_stride_token, num_blocks, cpu_bt, cpu_bt_stride,
+               std::max<int32_t>(width, 1), cpu_lens, n, num_heads, num_kv_heads, head_size,
+               block_size, scale, kv_dtype, out, row, head_size, FD_F32, lse, n, num_threads};
+    *call = runner().submit(c);
+    return FD_OK;
+  });
 }
 
 }  // extern "C"

@@ -40,6 +40,7 @@
 #include <atomic>
 #include <cmath>
 #include <condition_variable>
+#include <exception>
 #include <functional>
 #include <mutex>
 #include <thread>
@@ -54,7 +55,9 @@ namespace {
 
 // ---------------------------------------------------------------- pool
 // A persistent pool: run(n, f) calls f(w) for w = 0 .. n-1 on n threads (the
-// caller is worker 0) and returns when all of them have returned.
+// caller is worker 0) and returns when all of them have returned. The first
+// exception any of them throws (no memory for its scratch, say) is rethrown
+// on the caller's thread once all have returned.
 class Pool {
  public:
   void run(int n, const std::function<void(int)>& f) {
@@ -63,13 +66,23 @@ class Pool {
     job_ = &f;
     want_ = n - 1;
     active_ = n - 1;
+    error_ = nullptr;
     ++gen_;
     lk.unlock();
     cv_.notify_all();
-    f(0);
+    std::exception_ptr mine;
+    try {
+      f(0);
+    } catch (...) {
+      mine = std::current_exception();
+    }
     lk.lock();
     done_.wait(lk, [&] { return active_ == 0; });
     job_ = nullptr;
+    std::exception_ptr e = mine ? mine : error_;
+    error_ = nullptr;
+    lk.unlock();
+    if (e) std::rethrow_exception(e);
   }
 
   ~Pool() {
@@ -99,8 +112,14 @@ class Pool {
       if (id > want_) continue;  // not part of this run
       const std::function<void(int)>* f = job_;
       lk.unlock();
-      (*f)(id);
+      std::exception_ptr e;
+      try {
+        (*f)(id);
+      } catch (...) {
+        e = std::current_exception();
+      }
       lk.lock();
+      if (e && !error_) error_ = e;
       if (--active_ == 0) done_.notify_one();
     }
   }
@@ -109,6 +128,7 @@ class Pool {
   std::condition_variable cv_, done_;
   std::vector<std::thread> threads_;
   const std::function<void(int)>* job_ = nullptr;
+  std::exception_ptr error_;  // the first exception of a worker in the current run
   uint64_t gen_ = 0;
   int want_ = 0, active_ = 0;
   bool stop_ = false;
@@ -596,42 +616,44 @@ extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 // checksum (order independent).
 extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_threads,
                                    uint64_t* checksum) {
-  if (bytes % 64 != 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
-    return set_error(FD_ERR_INVALID, "fd_host_stream_read: bytes %% 64 != 0 or bad thread count");
-  if (bytes > 0 && (src == nullptr || reinterpret_cast<uintptr_t>(src) % 64 != 0))
-    return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL or unaligned (64 B) source");
-  if (checksum == nullptr) return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL checksum");
-  *checksum = 0;
-  if (bytes == 0) return FD_OK;
-  constexpr size_t kChunk = 1 << 20;
-  const int64_t chunks = (int64_t)((bytes + kChunk - 1) / kChunk);
-  const int nt = (int)std::max<int64_t>(
-      1, std::min<int64_t>(num_threads > 0 ? num_threads : default_threads(), chunks));
-  std::atomic<int64_t> next{0};
-  std::atomic<uint64_t> total{0};
-  const uint64_t* words = static_cast<const uint64_t*>(src);
-  const bool avx2 = isa_bits() != 0;
-  PoolState& ps = pool_state();
-  std::lock_guard<std::mutex> call(ps.call_mu);
-  ps.pool.run(nt, [&](int) {
-    uint64_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (;;) {
-      const int64_t c = next.fetch_add(1, std::memory_order_relaxed);
-      if (c >= chunks) break;
-      const size_t lo = (size_t)c * kChunk;
-      const size_t hi = std::min(bytes, (size_t)(c + 1) * kChunk);
-      if (avx2) {
-        x[0] ^= read_avx2::xor_lines(static_cast<const char*>(src), lo, hi);
-        continue;
+  return guarded("fd_host_stream_read", [&]() -> int {
+    if (bytes % 64 != 0 || num_threads < 0 || num_threads > FD_HOST_MAX_THREADS)
+      return set_error(FD_ERR_INVALID, "fd_host_stream_read: bytes %% 64 != 0 or bad thread count");
+    if (bytes > 0 && (src == nullptr || reinterpret_cast<uintptr_t>(src) % 64 != 0))
+      return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL or unaligned (64 B) source");
+    if (checksum == nullptr) return set_error(FD_ERR_INVALID, "fd_host_stream_read: NULL checksum");
+    *checksum = 0;
+    if (bytes == 0) return FD_OK;
+    constexpr size_t kChunk = 1 << 20;
+    const int64_t chunks = (int64_t)((bytes + kChunk - 1) / kChunk);
+    const int nt = (int)std::max<int64_t>(
+        1, std::min<int64_t>(num_threads > 0 ? num_threads : default_threads(), chunks));
+    std::atomic<int64_t> next{0};
+    std::atomic<uint64_t> total{0};
+    const uint64_t* words = static_cast<const uint64_t*>(src);
+    const bool avx2 = isa_bits() != 0;
+    PoolState& ps = pool_state();
+    std::lock_guard<std::mutex> call(ps.call_mu);
+    ps.pool.run(nt, [&](int) {
+      uint64_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+      for (;;) {
+        const int64_t c = next.fetch_add(1, std::memory_order_relaxed);
+        if (c >= chunks) break;
+        const size_t lo = (size_t)c * kChunk;
+        const size_t hi = std::min(bytes, (size_t)(c + 1) * kChunk);
+        if (avx2) {
+          x[0] ^= read_avx2::xor_lines(static_cast<const char*>(src), lo, hi);
+          continue;
+        }
+        for (size_t w = lo / 8; w < hi / 8; w += 8)
+          for (int j = 0; j < 8; ++j) x[j] ^= words[w + j];
       }
-      for (size_t w = lo / 8; w < hi / 8; w += 8)
-        for (int j = 0; j < 8; ++j) x[j] ^= words[w + j];
-    }
-    total.fetch_xor(x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7],
-                    std::memory_order_relaxed);
+      total.fetch_xor(x[0] ^ x[1] ^ x[2] ^ x[3] ^ x[4] ^ x[5] ^ x[6] ^ x[7],
+                      std::memory_order_relaxed);
+    });
+    *checksum = total.load(std::memory_order_relaxed);
+    return FD_OK;
   });
-  *checksum = total.load(std::memory_order_relaxed);
-  return FD_OK;
 }
 
 namespace fd {
@@ -674,36 +696,38 @@ extern "C" int fd_host_decode_partial(
     int32_t block_size, float scale, int32_t kv_dtype, void* out, int64_t out_stride_seq,
     int64_t out_stride_head, int32_t out_dtype, float* lse, int64_t lse_stride_head,
     int32_t num_threads) {
-  const int rc = host_decode_check(q, k_cache, v_cache, num_blocks, block_table, bt_stride,
-                                   bt_width, lens, n, num_heads, num_kv_heads, head_size,
-                                   block_size, scale, kv_dtype, out, out_dtype, lse, num_threads);
-  if (rc != FD_OK || n == 0) return rc;
-  int bits = isa_bits();
-  if (bits == 512 && use_bf16_dot()) bits = 513;  // internal tag of the bf16-dot body
-  const HostArgs a{q, q_stride_seq, q_stride_head, k_cache, v_cache, kv_stride_block,
-                   kv_stride_head, kv_stride_token, num_blocks, block_table, bt_stride, bt_width,
-                   lens, n, num_heads, num_kv_heads, head_size, block_size, scale, kv_dtype, out,
-                   out_stride_seq, out_stride_head, out_dtype, lse, lse_stride_head};
-  // work items (sequence, group of hg adjacent kv heads), longest sequences first
-  std::vector<int32_t> rows(n);
-  for (int i = 0; i < n; ++i) rows[i] = i;
-  std::stable_sort(rows.begin(), rows.end(), [&](int x, int y) { return lens[x] > lens[y]; });
-  const int want = num_threads > 0 ? num_threads : default_threads();
-  const int hg = item_heads(n, num_kv_heads, want);
-  const int groups = (num_kv_heads + hg - 1) / hg;
-  const int64_t items = (int64_t)n * groups;
-  const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(want, items));
-  std::atomic<int64_t> next{0};
-  PoolState& ps = pool_state();
-  std::lock_guard<std::mutex> call(ps.call_mu);
-  ps.pool.run(nt, [&](int) {
-    Scratch w;
-    for (;;) {
-      const int64_t it = next.fetch_add(1, std::memory_order_relaxed);
-      if (it >= items) break;
-      const int kh0 = (int)(it % groups) * hg;
-      run_item(a, rows[it / groups], kh0, std::min(hg, num_kv_heads - kh0), bits, w);
-    }
+  return guarded("fd_host_decode_partial", [&]() -> int {
+    const int rc = host_decode_check(q, k_cache, v_cache, num_blocks, block_table, bt_stride,
+                                     bt_width, lens, n, num_heads, num_kv_heads, head_size,
+                                     block_size, scale, kv_dtype, out, out_dtype, lse, num_threads);
+    if (rc != FD_OK || n == 0) return rc;
+    int bits = isa_bits();
+    if (bits == 512 && use_bf16_dot()) bits = 513;  // internal tag of the bf16-dot body
+    const HostArgs a{q, q_stride_seq, q_stride_head, k_cache, v_cache, kv_stride_block,
+                     kv_stride_head, kv_stride_token, num_blocks, block_table, bt_stride, bt_width,
+                     lens, n, num_heads, num_kv_heads, head_size, block_size, scale, kv_dtype, out,
+                     out_stride_seq, out_stride_head, out_dtype, lse, lse_stride_head};
+    // work items (sequence, group of hg adjacent kv heads), longest sequences first
+    std::vector<int32_t> rows(n);
+    for (int i = 0; i < n; ++i) rows[i] = i;
+    std::stable_sort(rows.begin(), rows.end(), [&](int x, int y) { return lens[x] > lens[y]; });
+    const int want = num_threads > 0 ? num_threads : default_threads();
+    const int hg = item_heads(n, num_kv_heads, want);
+    const int groups = (num_kv_heads + hg - 1) / hg;
+    const int64_t items = (int64_t)n * groups;
+    const int nt = (int)std::max<int64_t>(1, std::min<int64_t>(want, items));
+    std::atomic<int64_t> next{0};
+    PoolState& ps = pool_state();
+    std::lock_guard<std::mutex> call(ps.call_mu);
+    ps.pool.run(nt, [&](int) {
+      Scratch w;
+      for (;;) {
+        const int64_t it = next.fetch_add(1, std::memory_order_relaxed);
+        if (it >= items) break;
+        const int kh0 = (int)(it % groups) * hg;
+        run_item(a, rows[it / groups], kh0, std::min(hg, num_kv_heads - kh0), bits, w);
+      }
+    });
+    return FD_OK;
   });
-  return FD_OK;
 }
