@@ -604,8 +604,9 @@ int fd_host_decode_isa(void);
 
 /* Measurement helper: reads `bytes` (a multiple of 64) of host memory at src
  * (64-byte aligned) on num_threads host cores (0: as fd_host_decode_partial
- * picks them), in 1 MiB pieces streamed with prefetched 32-byte loads (the
- * way the host-core kernel reads its blocks), with no work per byte beyond
+ * picks them), in 1 MiB pieces, each read as four interleaved streams of
+ * prefetched 32-byte loads (one stream per core reads DRAM at about half
+ * its rate on some hosts), with no work per byte beyond
  * an XOR into *checksum (the XOR of all 64-bit words). Its rate is what the
  * host cores can stream from DRAM: the bound of the host-core leg of the
  * split step. No counterpart in

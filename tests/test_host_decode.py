@@ -262,14 +262,17 @@ def test_host_decode_in_a_forked_child():
 def test_host_stream_read_checksum_and_arguments():
     """fd_host_stream_read (the host-DRAM read-rate probe): the checksum is the
     XOR of the buffer's 64-bit words, whatever the thread count and whether
-    the size is a whole number of its 1 MiB chunks; bad sizes, unaligned
-    sources and too many threads are argument errors."""
+    the size is a whole number of its 1 MiB chunks or of the four interleaved
+    streams each chunk is read as (odd line counts per stream, lines past the
+    streams); bad sizes, unaligned sources and too many threads are argument
+    errors."""
     import numpy as np
 
     from vllm_fastdecoder_amd import _lib, ops
 
     g = torch.Generator().manual_seed(3)
-    for nbytes in (64, 4096, (3 << 20) + 192):
+    for nbytes in (64, 320, 576, 704, 832, 4096, (1 << 20) - 64, (2 << 20) + 13 * 64,
+                   (3 << 20) + 192):
         words = torch.randint(-(2 ** 62), 2 ** 62, (nbytes // 8,), generator=g, dtype=torch.int64)
         want = int(np.bitwise_xor.reduce(words.numpy().view(np.uint64)))
         for threads in (1, 3, 0):

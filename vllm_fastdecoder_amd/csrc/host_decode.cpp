@@ -414,29 +414,48 @@ struct V : isa_avx512::V512 {
 namespace read_avx2 {
 
 // XOR of the 64-bit words in bytes [lo, hi) of p (64-byte aligned, hi - lo a
-// multiple of 64), read with 32-byte loads into four independent chains, each
-// 64-byte line prefetched kAhead bytes before its load (the host-core kernel
-// prefetches its next block runs the same way: the hardware prefetchers
-// alone leave the cores' DRAM streams short of their rate).
+// multiple of 64), read as four interleaved streams over its four quarters
+// (each step takes 128 bytes of every stream with 32-byte loads), every line
+// prefetched kAhead bytes before its load. One stream per core with the
+// hardware prefetchers alone, or with a software prefetch, read the host's
+// DRAM at about half its rate on some hosts (202 against 403 GB/s on 16
+// cores); two to eight streams per core, or the host-core kernel's own
+// pattern (K and V runs of adjacent kv heads, the next ones prefetched),
+// reach it.
 uint64_t xor_lines(const char* p, size_t lo, size_t hi) {
-  constexpr size_t kAhead = 2048;
-  __m256i a = _mm256_setzero_si256(), b = a, c = a, d = a;
-  size_t o = lo;
-  for (; o + 128 <= hi; o += 128) {
-    if (o + kAhead + 128 <= hi) {
-      _mm_prefetch(p + o + kAhead, _MM_HINT_T0);
-      _mm_prefetch(p + o + kAhead + 64, _MM_HINT_T0);
+  constexpr int kStreams = 4;
+  constexpr size_t kAhead = 4096;
+  const size_t lines = (hi - lo) / 64;
+  const size_t len = lines / kStreams * 64;  // bytes of each stream (the rest: a tail)
+  __m256i acc[kStreams][2];
+  for (int k = 0; k < kStreams; ++k) acc[k][0] = acc[k][1] = _mm256_setzero_si256();
+  size_t o = 0;
+  for (; o + 128 <= len; o += 128) {
+    for (int k = 0; k < kStreams; ++k) {
+      const char* q = p + lo + k * len + o;
+      if (o + kAhead + 128 <= len) {
+        _mm_prefetch(q + kAhead, _MM_HINT_T0);
+        _mm_prefetch(q + kAhead + 64, _MM_HINT_T0);
+      }
+      const __m256i* v = reinterpret_cast<const __m256i*>(q);
+      acc[k][0] = _mm256_xor_si256(acc[k][0], _mm256_xor_si256(_mm256_load_si256(v),
+                                                                _mm256_load_si256(v + 1)));
+      acc[k][1] = _mm256_xor_si256(acc[k][1], _mm256_xor_si256(_mm256_load_si256(v + 2),
+                                                                _mm256_load_si256(v + 3)));
     }
-    a = _mm256_xor_si256(a, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o)));
-    b = _mm256_xor_si256(b, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 32)));
-    c = _mm256_xor_si256(c, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 64)));
-    d = _mm256_xor_si256(d, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 96)));
   }
-  if (o < hi) {  // a last 64-byte line
-    a = _mm256_xor_si256(a, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o)));
-    b = _mm256_xor_si256(b, _mm256_load_si256(reinterpret_cast<const __m256i*>(p + o + 32)));
+  __m256i x = _mm256_setzero_si256();
+  for (int k = 0; k < kStreams; ++k) {
+    if (o < len) {  // each stream's last 64-byte line (len an odd number of lines)
+      const __m256i* v = reinterpret_cast<const __m256i*>(p + lo + k * len + o);
+      x = _mm256_xor_si256(x, _mm256_xor_si256(_mm256_load_si256(v), _mm256_load_si256(v + 1)));
+    }
+    x = _mm256_xor_si256(x, _mm256_xor_si256(acc[k][0], acc[k][1]));
   }
-  const __m256i x = _mm256_xor_si256(_mm256_xor_si256(a, b), _mm256_xor_si256(c, d));
+  for (size_t t = lo + kStreams * len; t < hi; t += 64) {  // lines past the four streams
+    const __m256i* v = reinterpret_cast<const __m256i*>(p + t);
+    x = _mm256_xor_si256(x, _mm256_xor_si256(_mm256_load_si256(v), _mm256_load_si256(v + 1)));
+  }
   return (uint64_t)_mm256_extract_epi64(x, 0) ^ (uint64_t)_mm256_extract_epi64(x, 1) ^
          (uint64_t)_mm256_extract_epi64(x, 2) ^ (uint64_t)_mm256_extract_epi64(x, 3);
 }
@@ -610,10 +629,10 @@ extern "C" int fd_host_decode_isa(void) { return isa_bits(); }
 
 // Plain multi-threaded read of a host buffer on the pool that runs the
 // host-core kernel: 1 MiB chunks handed out from an atomic counter, each
-// streamed with prefetched 32-byte loads into XOR chains (no other work per
-// byte; 64-bit words where AVX2 is missing), so the rate is the cores' DRAM
-// read rate for a streamed buffer. The XOR of all words comes back as a
-// checksum (order independent).
+// read as four interleaved prefetched streams of 32-byte loads into XOR
+// chains (no other work per byte; 64-bit words where AVX2 is missing), so the
+// rate is the cores' DRAM read rate for a streamed buffer. The XOR of all
+// words comes back as a checksum (order independent).
 extern "C" int fd_host_stream_read(const void* src, size_t bytes, int32_t num_threads,
                                    uint64_t* checksum) {
   return guarded("fd_host_stream_read", [&]() -> int {
