@@ -160,6 +160,10 @@ PoolState& pool_state() {
   return *st;
 }
 
+// How many (block, kv head) runs past the one being reduced the host-core
+// kernel prefetches (spread over that run's score loop).
+constexpr int kAheadRuns = 1;
+
 struct HostArgs {
   const void* q;
   int64_t q_ss, q_sh;

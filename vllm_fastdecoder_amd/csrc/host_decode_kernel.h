@@ -266,24 +266,24 @@ bool run_heads(const HostArgs& a, int i, int kh0, int nkh, int g0, Scratch& w) {
   const char* kbase = static_cast<const char*>(a.k);
   const char* vbase = static_cast<const char*>(a.v);
   const int32_t* row_bt = a.bt + (int64_t)i * a.bt_stride;
+  // the item's (block, kv head) runs in the order read: r = b * nkh + j
+  const int64_t runs = (int64_t)nb * nkh;
+  auto run_base = [&](int64_t r) -> int64_t {  // -1 past the row or at a bad id
+    if (r >= runs) return -1;
+    const int64_t id = row_bt[r / nkh];
+    if (id < 0 || id >= a.num_blocks) return -1;
+    return id * a.sb + (int64_t)(kh0 + r % nkh) * a.sh;
+  };
   for (int b = 0; b < nb; ++b) {
     const int64_t bid = row_bt[b];
     if (bid < 0 || bid >= a.num_blocks) return false;
     const int ntok = std::min(BS, L - b * BS);
-    // the next block's id, for the prefetch after the item's last kv head
-    int64_t next_bid = -1;
-    if (b + 1 < nb) {
-      const int64_t nid = row_bt[b + 1];
-      if (nid >= 0 && nid < a.num_blocks) next_bid = nid;
-    }
     for (int j = 0; j < nkh; ++j) {
       const int kh = kh0 + j;
       const int64_t base = bid * a.sb + (int64_t)kh * a.sh;
-      // the run read after this one, prefetched a few rows at a time below:
-      // the next kv head's run of this block, else the next block's first
-      const int64_t nbase = j + 1 < nkh    ? base + a.sh
-                            : next_bid >= 0 ? next_bid * a.sb + (int64_t)kh0 * a.sh
-                                            : -1;
+      // the run read kAheadRuns after this one, prefetched a few rows at a
+      // time below
+      const int64_t nbase = run_base((int64_t)b * nkh + j + kAheadRuns);
       int pf = 0;  // next row of that run to prefetch
       auto prefetch_rows = [&](int upto) {
         if (nbase < 0) return;
