@@ -847,7 +847,11 @@ def main() -> int:
     if args.workload == "vicuna7b" and not args.no_legs:
         for name, lcopies, graph in (("correctness", 5, True), ("llama3_8b", 1, False)):
             lw = cases.WORKLOADS[name]
-            ms_l, nb_l, kv_l, _, note = decode_leg(lw, "vllm", args.steps, args.warmup, dev,
+            # the small batch's graph holds at least 200 launches whatever
+            # --steps says (a decode step's graph holds every layer's): the
+            # gap between two replays is not a launch's time
+            lsteps = max(args.steps, 200) if graph else args.steps
+            ms_l, nb_l, kv_l, _, note = decode_leg(lw, "vllm", lsteps, args.warmup, dev,
                                                   copies=lcopies, graph=graph, min_warm_ms=100.0)
             key = "small_batch_leg" if name == "correctness" else "llama3_8b_leg"
             legs[key] = leg_summary(lw, "vllm", ms_l, nb_l, kv_l, note, copies=lcopies)
