@@ -810,7 +810,7 @@ def leg_summary(w, layout, ms, nbytes, kvb, note, copies=1):
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+        print(json.dumps({"error": "bench.py runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
         return 2
     import torch

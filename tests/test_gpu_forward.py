@@ -5,7 +5,7 @@ merge) against attention over one unified cache.
 Follows the reference's own forward tests (tests/test_plan_and_forward.py:
 123-256, 345-385): the prefill forms of OPS.fa (P and F rows, not on the
 decode path) are served by a float32 torch stand-in defined here, the decode
-partial by this build's HIP kernel. Tolerances: output 3e-3 max-abs for fp16
+partial by the library's HIP kernel. Tolerances: output 3e-3 max-abs for fp16
 (2e-3 attention error + fp16 rounding), 2e-2 for bf16, 1e-4 for fp32; both
 tiers bit-exact against the unified reference cache afterwards.
 """

@@ -8,7 +8,7 @@ blocks in pinned host memory [C, KVH, BS, D], read by the GPU zero-copy.
 
 The reference's split step is three calls: the GPU-tier partial, the
 host-tier partial and the LSE merge (fastdecode/backend.py:293-356; the same
-check in scripts/gpu_selftest.py:215-239). Each way this build runs that step
+check in scripts/gpu_selftest.py:215-239). Each way the library runs that step
 is compared, on every row, with the float64 oracle of monolithic attention
 over the row's blocks of both tiers as one list:
   * the three calls (paged_decode + decode_attn + merge_attn_states);

@@ -7,8 +7,8 @@ vLLM's base classes:
     `merge`, `event`), routed to libfdattn. `fa` implements the paged decode
     form the split path uses (one query token per row, block table,
     return_softmax_lse); prefill forms raise NotImplementedError (FlashAttention
-    prefill is not on this path). `split_decode` (this build's addition) is
-    the fused form of the S rows' two partials and their merge. Tests swap
+    prefill is not on this path). `split_decode` (no counterpart in the
+    reference) is the fused form of the S rows' two partials and their merge. Tests swap
     OPS the way the reference's tests do (tests/test_plan_and_forward.py:106-113).
   * `build_split_plan` -- FastDecodeMetadataBuilder.build (backend.py:140-178):
     one device-to-host copy of the step's block table and slots, the host
@@ -21,8 +21,8 @@ vLLM's base classes:
     share balanced online (`cpu_fraction="auto"`, the default); a layer with
     little host-tier KV, or `cpu_fraction=0`, leaves the whole host tier to
     the GPU with no host wait.
-  * `build_device_step` / `SplitDecodeImpl._forward_device` -- this build's
-    addition: the same step planned on the GPU (fd_plan_tiers), with no
+  * `build_device_step` / `SplitDecodeImpl._forward_device` -- no
+    counterpart in the reference: the same step planned on the GPU (fd_plan_tiers), with no
     device-to-host copy, for steps whose prefill rows (if any) are fresh.
 """
 
@@ -51,7 +51,7 @@ class HipOps:
         (backend.py:306-314): k/v are the [B, BS, KVH, D] cache views, one query
         token per row, seqused_k the per-row token counts (0 allowed),
         max_seqlen_k the longest of them (only the table columns it needs are
-        read). This build's additions: row_order schedules rows (e.g. longest
+        read). Beyond the reference's call: row_order schedules rows (e.g. longest
         first); total_tokens, the sum of seqused_k known on the host, lets the
         launch plan size tasks for rows of uneven length."""
         if block_table is None or max_seqlen_q != 1 or seqused_k is None:

@@ -818,7 +818,8 @@ def decode_attn(q, k_cache, v_cache, block_table, lens, scale, out, lse, row_ord
     q [n, H, D]; k_cache/v_cache [C, KVH, BS, D] (pinned host memory or HBM);
     block_table [n, W] int32 (tier-relative ids in sequence order); lens [n]
     int32; out [n, H, D] (q's dtype, or float32); lse [H, n] float32.
-    row_order: optional scheduling permutation (this build's addition).
+    row_order: optional scheduling permutation (no counterpart in the
+    reference).
     """
     _require(k_cache.dim() == 4 and v_cache.shape == k_cache.shape,
              "k_cache/v_cache must be [C, KVH, BS, D]")
@@ -962,8 +963,8 @@ def paged_decode(
     more than one sized to the batch. A row longer than max_seqlen_k is then a
     range error: its out and lse are NaN.
 
-    total_tokens (this build's addition: the sum of seqused_k, which a serving
-    step's scheduler knows on the host): lets the launch plan tell rows of
+    total_tokens (no counterpart in the reference: the sum of seqused_k,
+    which a serving step's scheduler knows on the host): lets the launch plan tell rows of
     uneven length from equal ones, which want different task sizes. Results
     do not depend on it.
 

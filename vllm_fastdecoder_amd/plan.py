@@ -62,7 +62,8 @@ class HostPlan:
     f_tok: torch.Tensor  # [nF_tok] int64
     f_cu: torch.Tensor  # [nF + 1] int32
     f_max: int
-    # this build: the step's slots rebased to the host tier, HBM slots -> -1
+    # (no counterpart in the reference) the step's slots rebased to the host
+    # tier, HBM slots -> -1
     host_slot_mapping: torch.Tensor | None = None  # [n_tok] int64
 
     @property
@@ -233,14 +234,15 @@ class DevicePlan:
     p_bt: torch.Tensor  # [nP, W] int32 rows of the batch block table
     s_tok: torch.Tensor
     # the S rows that hold HBM tokens (the reference hands only these to
-    # FlashAttention; this build's kernel also accepts empty rows)
+    # FlashAttention; the HIP kernel here also accepts empty rows)
     s_gpu_rows: torch.Tensor  # [nG] int64, indices into the S rows
     s_gpu_cu: torch.Tensor  # arange(nG + 1) int32
     s_gpu_bt: torch.Tensor  # [nG, Wg] int32
     s_gpu_lens: torch.Tensor  # [nG] int32, all > 0
     f_tok: torch.Tensor
     f_cu: torch.Tensor
-    # this build: every S row's tables on the device, and the host-tier writes
+    # (no counterpart in the reference) every S row's tables on the device,
+    # and the host-tier writes
     s_gpu_bt_all: torch.Tensor | None = None  # [nS, Wg] int32
     s_gpu_lens_all: torch.Tensor | None = None  # [nS] int32
     s_cpu_bt: torch.Tensor | None = None  # [nS, Wc] int32
