@@ -189,14 +189,25 @@ def decode_plan_info(n: int, H: int, KVH: int, D: int, BS: int, width: int, dtyp
             "wave_blocks": plan.wave_blocks}
 
 
+_GET_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _current_device() -> int:
+    """Index of the current device (-1 without one); the raw query where torch
+    has it, as a decode call's workspace lookup runs on every launch."""
+    if _GET_DEVICE is not None and torch.cuda.is_initialized():
+        return int(_GET_DEVICE())
+    return torch.cuda.current_device() if torch.cuda.is_available() else -1
+
+
 def workspace_bytes(n: int, H: int, KVH: int, D: int, BS: int, width: int) -> int:
     """Workspace a decode call of this shape needs on the current device
     (remembered per shape, device and the planner overrides it depends on:
     FD_SPLIT_BLOCKS, and FD_DECODE_KERNEL, which can allow more splits; the
     device's CU count sets the split bounds)."""
-    dev = torch.cuda.current_device() if torch.cuda.is_available() else -1
-    key = (n, H, KVH, D, BS, width, os.environ.get("FD_SPLIT_BLOCKS"),
-           os.environ.get("FD_DECODE_KERNEL"), dev)
+    env = os.environ
+    key = (n, H, KVH, D, BS, width, env.get("FD_SPLIT_BLOCKS"), env.get("FD_DECODE_KERNEL"),
+           _current_device())
     size = _WS_SIZES.get(key)
     if size is None:
         c = ctypes.c_size_t()
